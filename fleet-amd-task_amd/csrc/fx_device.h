@@ -1,0 +1,199 @@
+// Device primitives of the gfx950 decode path: bf16, the FP32 arithmetic spec (fixed summation
+// orders, own exp/log), coherent (agent-scope, sc1) activation access and weight streaming.
+//
+// Arithmetic spec shared with the CPU oracle (oracle/fleet_oracle.c), all FP32 IEEE RNE, compiled
+// with -ffp-contract=off so every written multiply and add rounds on its own:
+//   bf16r        round to nearest even                      (harness/numpy_ref.py:36-42)
+//   dot_lanes    chunk c of 8 contiguous elements -> lane c % 64, one fma per element in increasing
+//                c, then an xor butterfly over min(64, pow2ceil(chunks)) lanes, offsets 1, 2, .., 32
+//   exp_s/log_s  Cody-Waite range reduction + Taylor polynomial (below)
+//   silu_s       x / (1 + exp_s(-x))                           (harness/numpy_ref.py:248-253)
+//
+// Coherence model (measured on MI355X): the eight XCD L2s are not coherent with each other and the
+// agent-scope fences (buffer_wbl2 / buffer_inv) cost microseconds when 256 workgroups issue them.
+// Every value one workgroup writes and another reads is therefore stored and loaded with the sc1
+// cache policy (agent-coherent, bypassing the non-coherent cache levels) and ordered with
+// s_waitcnt; weights and other read-only tensors use ordinary (non-temporal) loads.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define FX_THREADS 256
+#define FX_WAVES 4
+#define FX_XCDS 8
+#define FX_LDS_BYTES (96 * 1024)
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// ------------------------------------------------------------------------------------------------
+// bf16
+
+__device__ __forceinline__ float bf2f(uint32_t u16) { return __uint_as_float(u16 << 16); }
+__device__ __forceinline__ float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+__device__ __forceinline__ uint32_t f2bf(float f) {
+  uint32_t u = __float_as_uint(f);
+  u = u + 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+__device__ __forceinline__ float bf16r(float f) { return bf2f(f2bf(f)); }
+__device__ __forceinline__ uint32_t pack2(float lo, float hi) { return f2bf(lo) | (f2bf(hi) << 16); }
+
+// ------------------------------------------------------------------------------------------------
+// spec exp / log / silu (identical operation sequence to oracle/fleet_oracle.c)
+
+__device__ __forceinline__ float exp_s(float x) {
+  if (!(x >= -87.0f)) return 0.0f;
+  if (x > 88.0f) return __uint_as_float(0x7f800000u);
+  const float LOG2E = 1.44269504088896341f;
+  const float LN2_HI = 0.693145751953125f;
+  const float LN2_LO = 1.42860682030941723e-06f;
+  float t = x * LOG2E;
+  float n = __builtin_rintf(t);
+  float r = x - n * LN2_HI;
+  r = r - n * LN2_LO;
+  float p = 1.3888889e-3f;
+  p = p * r + 8.3333333e-3f;
+  p = p * r + 4.1666668e-2f;
+  p = p * r + 1.6666667e-1f;
+  p = p * r + 0.5f;
+  p = p * r + 1.0f;
+  p = p * r + 1.0f;
+  int ni = (int)n;
+  float scale = __uint_as_float((uint32_t)(ni + 127) << 23);
+  return p * scale;
+}
+
+__device__ __forceinline__ float log_s(float x) {
+  uint32_t u = __float_as_uint(x);
+  int e = (int)((u >> 23) & 0xffu) - 127;
+  float m = __uint_as_float((u & 0x007fffffu) | 0x3f800000u);
+  if (m > 1.41421356f) { m = m * 0.5f; e = e + 1; }
+  float f = m - 1.0f;
+  float s = f / (2.0f + f);
+  float z = s * s;
+  float p = 0.22222222f;
+  p = p * z + 0.28571429f;
+  p = p * z + 0.4f;
+  p = p * z + 0.66666669f;
+  p = p * z + 2.0f;
+  float lm = s * p;
+  const float LN2 = 0.693147182f;
+  return (float)e * LN2 + lm;
+}
+
+__device__ __forceinline__ float silu_s(float x) { return x / (1.0f + exp_s(-x)); }
+
+// ------------------------------------------------------------------------------------------------
+// coherent (sc1) access to activations through buffer resources; byte offsets
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* p) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, 0x7fffffff, 0x00020000);
+}
+#define FX_SC1 16
+__device__ __forceinline__ u32x4 ldc16(const void* base, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(rsrc(base), off, 0, FX_SC1);
+}
+__device__ __forceinline__ u32x2 ldc8(const void* base, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b64(rsrc(base), off, 0, FX_SC1);
+}
+__device__ __forceinline__ uint32_t ldc4(const void* base, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b32(rsrc(base), off, 0, FX_SC1);
+}
+__device__ __forceinline__ uint32_t ldc2(const void* base, uint32_t off) {
+  return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rsrc(base), off, 0, FX_SC1);
+}
+__device__ __forceinline__ void stc16(void* base, uint32_t off, u32x4 v) {
+  __builtin_amdgcn_raw_buffer_store_b128(v, rsrc(base), off, 0, FX_SC1);
+}
+__device__ __forceinline__ void stc8(void* base, uint32_t off, u32x2 v) {
+  __builtin_amdgcn_raw_buffer_store_b64(v, rsrc(base), off, 0, FX_SC1);
+}
+__device__ __forceinline__ void stc4(void* base, uint32_t off, uint32_t v) {
+  __builtin_amdgcn_raw_buffer_store_b32(v, rsrc(base), off, 0, FX_SC1);
+}
+__device__ __forceinline__ void stc2(void* base, uint32_t off, uint32_t v) {
+  __builtin_amdgcn_raw_buffer_store_b16((unsigned short)v, rsrc(base), off, 0, FX_SC1);
+}
+__device__ __forceinline__ float ldcf(const void* base, uint32_t idx) { return __uint_as_float(ldc4(base, idx * 4)); }
+__device__ __forceinline__ void stcf(void* base, uint32_t idx, float v) { stc4(base, idx * 4, __float_as_uint(v)); }
+
+// flags (agent scope, relaxed)
+__device__ __forceinline__ uint32_t flag_ld(const uint32_t* p) {
+  return __hip_atomic_load(const_cast<uint32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void flag_st(uint32_t* p, uint32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void wait_mem() { __builtin_amdgcn_s_waitcnt(0); }
+
+// weights: read-only for the whole dispatch, streamed once -> non-temporal 16-byte loads
+__device__ __forceinline__ u32x4 ldw16(const void* p) { return __builtin_nontemporal_load((const u32x4*)p); }
+__device__ __forceinline__ u32x4 ld16(const void* p) { return *(const u32x4*)p; }
+
+// ------------------------------------------------------------------------------------------------
+// identity
+
+__device__ __forceinline__ uint32_t xcc_id() {
+  uint32_t x;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(x));
+  return x & 15u;
+}
+__device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
+__device__ __forceinline__ int wave_id() { return threadIdx.x >> 6; }
+
+// ------------------------------------------------------------------------------------------------
+// reductions
+
+__device__ __forceinline__ float shfl_xor_f(float v, int m) { return __shfl_xor(v, m, 64); }
+
+// xor butterfly over the lowest `nl` lanes of each 64-lane group (spec order 1, 2, 4, ..)
+__device__ __forceinline__ float butterfly(float v, int nl) {
+  for (int off = 1; off < nl; off <<= 1) v = v + shfl_xor_f(v, off);
+  return v;
+}
+__device__ __forceinline__ float butterfly64(float v) {
+  v = v + shfl_xor_f(v, 1);
+  v = v + shfl_xor_f(v, 2);
+  v = v + shfl_xor_f(v, 4);
+  v = v + shfl_xor_f(v, 8);
+  v = v + shfl_xor_f(v, 16);
+  v = v + shfl_xor_f(v, 32);
+  return v;
+}
+__device__ __forceinline__ int lanes_for(int nchunk) {
+  int nl = 1;
+  while (nl < nchunk && nl < 64) nl <<= 1;
+  return nl;
+}
+__device__ __forceinline__ float wave_max(float v) {
+  for (int off = 1; off < 64; off <<= 1) v = fmaxf(v, shfl_xor_f(v, off));
+  return v;
+}
+
+// 8 fma of a bf16 chunk (4 words) with 8 f32 values, chunk order e = 0..7
+__device__ __forceinline__ float fma8(u32x4 w, const float* x, float acc) {
+  acc = __builtin_fmaf(bf_lo(w.x), x[0], acc);
+  acc = __builtin_fmaf(bf_hi(w.x), x[1], acc);
+  acc = __builtin_fmaf(bf_lo(w.y), x[2], acc);
+  acc = __builtin_fmaf(bf_hi(w.y), x[3], acc);
+  acc = __builtin_fmaf(bf_lo(w.z), x[4], acc);
+  acc = __builtin_fmaf(bf_hi(w.z), x[5], acc);
+  acc = __builtin_fmaf(bf_lo(w.w), x[6], acc);
+  acc = __builtin_fmaf(bf_hi(w.w), x[7], acc);
+  return acc;
+}
+
+// dot_lanes of a vector held in LDS (f32, K values) with itself: one wave, result on all lanes
+__device__ __forceinline__ float sumsq_wave(const float* xs, int K) {
+  const int lane = lane_id();
+  const int nchunk = K >> 3;
+  float acc = 0.0f;
+  for (int c = lane; c < nchunk; c += 64) {
+    const float* p = xs + c * 8;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc = __builtin_fmaf(p[e], p[e], acc);
+  }
+  return butterfly(acc, lanes_for(nchunk));
+}

@@ -1,0 +1,587 @@
+// Persistent decode runtime for gfx950 (MI355X) and the C ABI of include/fleet_mi355x.h.
+//
+// One launch of 256 workgroups, one per CU (the 96 KiB of dynamic LDS each admits one per CU), with
+// blockIdx b on XCD b % 8 (checked at fx_create). Rank 0 of each XCD (blocks 0..7) is that XCD's
+// scheduler: it aggregates the epoch flags of the XCD's 31 workers and, for a device-wide sync,
+// exchanges one flag per XCD with the other seven schedulers, then releases its workers. The
+// workers (blocks 8..255) walk the task table, iteration by iteration, running their share of each
+// stage (fx_ops.h) and announcing completion through their own flag. No counter is shared by more
+// than one writer (same-address atomics serialise at ~150 ns each on this part) and no cache
+// maintenance instruction is issued: everything exchanged between workgroups travels through
+// sc1 (agent-coherent) loads and stores, ordered by s_waitcnt.
+//
+// Replaces the fork runtime's prepare / scheduler / worker kernels and event counters
+// (docs/fleet/03-runtime.md:125-313, fleet/patches/sched_xcd.patch) with a static task table.
+#include <hip/hip_runtime.h>
+#include <cstdio>
+#include <cstring>
+#include <cstdlib>
+#include <string>
+#include <vector>
+
+#include "fx_ops.h"
+
+#define FX_BLOCKS 256
+static_assert(sizeof(fx_stage) == 200, "fx_stage layout is part of the ABI (fleet/runtime.py FxStage)");
+#define FX_WORKERS 248
+#define FX_XWORKERS 31
+// a wait that has not been satisfied after this many s_memrealtime ticks (100 MHz) declares the
+// run failed: every wait then returns, so the grid drains instead of hanging
+#define FX_WAIT_TICKS (200ull * 1000 * 1000)
+
+struct FxRunArgs {
+  const fx_stage* stages;
+  int n_stages;
+  const fx_stage* epi;
+  int n_epi;
+  int iters, step0, n_prompt;
+  int64_t* tokens;
+  uint32_t* sync;
+  uint64_t* timing;
+  uint32_t epoch0;
+};
+
+__device__ __forceinline__ bool timed_out(uint64_t t0, uint32_t* sync) {
+  if (__builtin_amdgcn_s_memrealtime() - t0 > FX_WAIT_TICKS) {
+    flag_st(&sync[FX_FLAG_ERROR], 1u);
+    return true;
+  }
+  return flag_ld(&sync[FX_FLAG_ERROR]) != 0u;
+}
+
+// worker side of a sync: publish the epoch, wait for the scheduler's go
+__device__ __forceinline__ void worker_sync(uint32_t* sync, int b, uint32_t epoch) {
+  wait_mem();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    flag_st(&sync[FX_FLAG_ARRIVE(b)], epoch);
+    uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+    uint32_t spins = 0;
+    while (flag_ld(&sync[FX_FLAG_GO(b)]) < epoch) {
+      if ((++spins & 255u) == 0 && timed_out(t0, sync)) break;
+    }
+  }
+  __syncthreads();
+}
+
+// scheduler side (wave 0 of block x): gather the XCD's workers, optionally all XCDs, release
+__device__ __forceinline__ void scheduler_sync(uint32_t* sync, int x, uint32_t epoch, bool global) {
+  const int lane = lane_id();
+  const int wb = (lane + 1) * 8 + x;   // block of worker `lane` of this XCD (lane < 31)
+  uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+  uint32_t spins = 0;
+  bool ok;
+  do {
+    ok = lane >= FX_XWORKERS || flag_ld(&sync[FX_FLAG_ARRIVE(wb)]) >= epoch;
+    ok = __all(ok);
+    if (!ok && (++spins & 63u) == 0 && timed_out(t0, sync)) break;
+  } while (!ok);
+  if (global) {
+    if (lane == 0) flag_st(&sync[FX_FLAG_XCD(x)], epoch);
+    do {
+      ok = lane >= FX_XCDS || flag_ld(&sync[FX_FLAG_XCD(lane)]) >= epoch;
+      ok = __all(ok);
+      if (!ok && (++spins & 63u) == 0 && timed_out(t0, sync)) break;
+    } while (!ok);
+  }
+  if (lane < FX_XWORKERS) flag_st(&sync[FX_FLAG_GO(wb)], epoch);
+}
+
+__global__ void __launch_bounds__(FX_THREADS) fx_persistent(FxRunArgs a) {
+  extern __shared__ __attribute__((aligned(16))) char lds[];
+  const int b = blockIdx.x;
+  const int x = b & 7, rank = b >> 3;
+  if (rank == 0) {
+    if (wave_id() != 0) return;
+    uint32_t epoch = a.epoch0;
+    for (int it = 0; it < a.iters; ++it)
+      for (int s = 0; s < a.n_stages; ++s) {
+        const int sy = a.stages[s].sync;
+        if (sy != FX_SYNC_NONE) scheduler_sync(a.sync, x, ++epoch, sy == FX_SYNC_GLOBAL);
+      }
+    for (int s = 0; s < a.n_epi; ++s) {
+      const int sy = a.epi[s].sync;
+      if (sy != FX_SYNC_NONE) scheduler_sync(a.sync, x, ++epoch, sy == FX_SYNC_GLOBAL);
+    }
+    return;
+  }
+  FxEnv env;
+  env.xcd = x;
+  env.xrank = rank - 1;
+  env.xworkers = FX_XWORKERS;
+  env.worker = env.xrank * 8 + x;
+  env.nworkers = FX_WORKERS;
+  env.n_prompt = a.n_prompt;
+  env.tokens = a.tokens;
+  env.sync = a.sync;
+  env.lds = lds;
+  uint32_t epoch = a.epoch0;
+  // the current stage descriptor is staged in LDS (read by every wave, never spilled to scratch)
+  fx_stage* sst = (fx_stage*)(lds + LDS_STAGE);
+  auto stage_in = [&](const fx_stage* src) {
+    __syncthreads();
+    if (threadIdx.x < sizeof(fx_stage) / 4) ((uint32_t*)sst)[threadIdx.x] = ((const uint32_t*)src)[threadIdx.x];
+    __syncthreads();
+  };
+  for (int it = 0; it < a.iters; ++it) {
+    env.iter = it;
+    env.step = a.step0 + it;
+    if (env.worker == 0 && threadIdx.x == 0 && a.timing) a.timing[it] = __builtin_amdgcn_s_memrealtime();
+    for (int s = 0; s < a.n_stages; ++s) {
+      stage_in(a.stages + s);
+      const int sync_kind = sst->sync;
+      const bool skip = (sst->flags & FX_F_HEAD) && (env.step + 1 < env.n_prompt);
+      if (!skip) run_stage(*sst, env);
+      if (sync_kind != FX_SYNC_NONE) worker_sync(a.sync, b, ++epoch);
+    }
+  }
+  env.iter = a.iters - 1;
+  env.step = a.step0 + a.iters - 1;
+  for (int s = 0; s < a.n_epi; ++s) {
+    stage_in(a.epi + s);
+    const int sync_kind = sst->sync;
+    run_stage(*sst, env);
+    if (sync_kind != FX_SYNC_NONE) worker_sync(a.sync, b, ++epoch);
+  }
+  if (env.worker == 0 && threadIdx.x == 0 && a.timing) a.timing[a.iters] = __builtin_amdgcn_s_memrealtime();
+}
+
+// one stage as a standalone launch (kernel suite): same work split, no syncs
+__global__ void __launch_bounds__(FX_THREADS) fx_stage_kernel(fx_stage st, int step, int iter, int n_prompt,
+                                                            int64_t* tokens, uint32_t* sync) {
+  extern __shared__ __attribute__((aligned(16))) char lds[];
+  const int b = blockIdx.x;
+  const int x = b & 7, rank = b >> 3;
+  if (rank == 0) return;
+  FxEnv env;
+  env.xcd = x;
+  env.xrank = rank - 1;
+  env.xworkers = FX_XWORKERS;
+  env.worker = env.xrank * 8 + x;
+  env.nworkers = FX_WORKERS;
+  env.n_prompt = n_prompt;
+  env.tokens = tokens;
+  env.sync = sync;
+  env.lds = lds;
+  env.iter = iter;
+  env.step = step;
+  run_stage(st, env);
+}
+
+__global__ void fx_xcc_map(uint32_t* out) {
+  extern __shared__ char lds[];
+  lds[threadIdx.x] = 0;
+  if (threadIdx.x == 0) out[blockIdx.x] = xcc_id();
+}
+
+// ------------------------------------------------------------------------------------------------
+// seeded generator: Philox4x32-10 (Salmon et al., SC'11) + Box-Muller with the spec's log and a
+// polynomial sin/cos on the quadrant-reduced angle; the CPU oracle implements the same sequence.
+
+__device__ __forceinline__ void philox(uint64_t seed, uint64_t block, uint32_t stream, uint32_t out[4]) {
+  uint32_t c0 = (uint32_t)block, c1 = (uint32_t)(block >> 32), c2 = stream, c3 = 0x5EEDu;
+  uint32_t k0 = (uint32_t)seed, k1 = (uint32_t)(seed >> 32);
+#pragma unroll
+  for (int r = 0; r < 10; ++r) {
+    uint64_t p0 = (uint64_t)0xD2511F53u * c0, p1 = (uint64_t)0xCD9E8D57u * c2;
+    uint32_t n0 = (uint32_t)(p1 >> 32) ^ c1 ^ k0;
+    uint32_t n1 = (uint32_t)p1;
+    uint32_t n2 = (uint32_t)(p0 >> 32) ^ c3 ^ k1;
+    uint32_t n3 = (uint32_t)p0;
+    c0 = n0; c1 = n1; c2 = n2; c3 = n3;
+    if (r < 9) { k0 += 0x9E3779B9u; k1 += 0xBB67AE85u; }
+  }
+  out[0] = c0; out[1] = c1; out[2] = c2; out[3] = c3;
+}
+
+__device__ __forceinline__ void sincos_quarter(float f, float* s, float* c) {
+  const float HALF_PI = 1.57079637f;
+  float t = f * HALF_PI;
+  float z = t * t;
+  float ps = -2.5052108e-8f;
+  ps = ps * z + 2.7557319e-6f;
+  ps = ps * z + -1.9841270e-4f;
+  ps = ps * z + 8.3333333e-3f;
+  ps = ps * z + -1.6666667e-1f;
+  ps = ps * z + 1.0f;
+  *s = ps * t;
+  float pc = 2.0876757e-9f;
+  pc = pc * z + -2.7557319e-7f;
+  pc = pc * z + 2.4801587e-5f;
+  pc = pc * z + -1.3888889e-3f;
+  pc = pc * z + 4.1666668e-2f;
+  pc = pc * z + -0.5f;
+  pc = pc * z + 1.0f;
+  *c = pc;
+}
+
+__device__ __forceinline__ void box_muller(uint32_t a, uint32_t b, float* z0, float* z1) {
+  const float INV24 = 5.96046448e-08f;
+  float u1 = (float)((a >> 8) + 1u) * INV24;
+  float u2 = (float)(b >> 8) * INV24;
+  float r = sqrtf(-2.0f * log_s(u1));
+  float v = u2 * 4.0f;
+  int q = (int)v;
+  float f = v - (float)q;
+  float s, c;
+  sincos_quarter(f, &s, &c);
+  float cs, sn;
+  switch (q) {
+    case 0: cs = c; sn = s; break;
+    case 1: cs = -s; sn = c; break;
+    case 2: cs = -c; sn = -s; break;
+    default: cs = s; sn = -c; break;
+  }
+  *z0 = r * cs;
+  *z1 = r * sn;
+}
+
+// contiguous source range [offset, offset + n): one thread per Philox block of 4 elements
+__global__ void fx_gen_kernel(uint16_t* dst, uint64_t n, uint64_t seed, uint32_t stream, float scale, uint64_t offset) {
+  const uint64_t first = offset & ~3ull;
+  const uint64_t nblocks = (offset + n - first + 3) / 4;
+  for (uint64_t bk = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; bk < nblocks; bk += (uint64_t)gridDim.x * blockDim.x) {
+    const uint64_t base = first + bk * 4;
+    uint32_t r[4];
+    philox(seed, base >> 2, stream, r);
+    float z[4];
+    box_muller(r[0], r[1], &z[0], &z[1]);
+    box_muller(r[2], r[3], &z[2], &z[3]);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const uint64_t i = base + k;
+      if (i < offset || i >= offset + n) continue;
+      dst[i - offset] = (uint16_t)f2bf(z[k] * scale);
+    }
+  }
+}
+
+// strided rows: one thread per element (each regenerates its Philox block)
+__global__ void fx_gen2d_kernel(uint16_t* dst, uint64_t rows, uint64_t row_len, uint64_t dst_stride, uint64_t src_offset,
+                                uint64_t src_stride, uint64_t seed, uint32_t stream, float scale) {
+  const uint64_t total = rows * row_len;
+  for (uint64_t e = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += (uint64_t)gridDim.x * blockDim.x) {
+    const uint64_t r = e / row_len, j = e % row_len;
+    const uint64_t i = src_offset + r * src_stride + j;
+    uint32_t w[4];
+    philox(seed, i >> 2, stream, w);
+    float z[4];
+    box_muller(w[0], w[1], &z[0], &z[1]);
+    box_muller(w[2], w[3], &z[2], &z[3]);
+    dst[r * dst_stride + j] = (uint16_t)f2bf(z[i & 3] * scale);
+  }
+}
+
+__global__ void fx_fill_kernel(uint16_t* dst, uint64_t n, uint16_t v) {
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (uint64_t)gridDim.x * blockDim.x) dst[i] = v;
+}
+
+// ------------------------------------------------------------------------------------------------
+// C ABI
+
+struct fx_ctx {
+  int device;
+  int cus;
+  std::string err;
+  uint32_t* sync = nullptr;
+  uint64_t* timing = nullptr;
+  int timing_cap = 0;
+  int last_iters = 0;
+  uint32_t epoch = 0;
+  fx_stage* d_stages = nullptr;
+  int n_stages = 0;
+  fx_stage* d_epi = nullptr;
+  int n_epi = 0;
+  std::vector<fx_stage> h_stages, h_epi;
+};
+
+static int fail(fx_ctx* c, int code, const std::string& msg) {
+  if (c) c->err = msg;
+  return code;
+}
+#define HIPCHK(c, x)                                                                    \
+  do {                                                                                  \
+    hipError_t e_ = (x);                                                                \
+    if (e_ != hipSuccess) return fail((c), FX_E_HIP, std::string(#x) + ": " + hipGetErrorString(e_)); \
+  } while (0)
+
+extern "C" {
+
+int fx_abi_version(void) { return FX_ABI_VERSION; }
+
+const char* fx_last_error(fx_ctx* c) { return c ? c->err.c_str() : "no context"; }
+
+int fx_create(int device, fx_ctx** out) {
+  if (!out) return FX_E_ARG;
+  *out = nullptr;
+  fx_ctx* c = new fx_ctx();
+  c->device = device;
+  hipError_t e = hipSetDevice(device);
+  if (e != hipSuccess) { delete c; return FX_E_HIP; }
+  hipDeviceProp_t pr;
+  if (hipGetDeviceProperties(&pr, device) != hipSuccess) { delete c; return FX_E_HIP; }
+  c->cus = pr.multiProcessorCount;
+  if (std::strncmp(pr.gcnArchName, "gfx950", 6) != 0 || pr.multiProcessorCount != FX_BLOCKS ||
+      pr.sharedMemPerBlock < (size_t)FX_LDS_BYTES) {
+    *out = c;
+    return fail(c, FX_E_DEVICE, std::string("expected a gfx950 with 256 CUs, got ") + pr.gcnArchName + " with " +
+                                    std::to_string(pr.multiProcessorCount) + " CUs");
+  }
+  *out = c;
+  HIPCHK(c, hipFuncSetAttribute((const void*)fx_persistent, hipFuncAttributeMaxDynamicSharedMemorySize, FX_LDS_BYTES));
+  HIPCHK(c, hipFuncSetAttribute((const void*)fx_stage_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, FX_LDS_BYTES));
+  HIPCHK(c, hipFuncSetAttribute((const void*)fx_xcc_map, hipFuncAttributeMaxDynamicSharedMemorySize, FX_LDS_BYTES));
+  HIPCHK(c, hipMalloc(&c->sync, FX_SYNC_WORDS * 4));
+  HIPCHK(c, hipMemset(c->sync, 0, FX_SYNC_WORDS * 4));
+  // the work split assumes block b runs on XCD b % 8 (round-robin dispatch); verify it once
+  uint32_t* d = nullptr;
+  HIPCHK(c, hipMalloc(&d, FX_BLOCKS * 4));
+  hipLaunchKernelGGL(fx_xcc_map, dim3(FX_BLOCKS), dim3(64), FX_LDS_BYTES, 0, d);
+  HIPCHK(c, hipGetLastError());
+  uint32_t h[FX_BLOCKS];
+  HIPCHK(c, hipMemcpy(h, d, sizeof(h), hipMemcpyDeviceToHost));
+  HIPCHK(c, hipFree(d));
+  for (int b = 0; b < FX_BLOCKS; ++b)
+    if (h[b] != (uint32_t)(b % 8))
+      return fail(c, FX_E_DEVICE, "block " + std::to_string(b) + " ran on XCD " + std::to_string(h[b]));
+  return FX_OK;
+}
+
+int fx_destroy(fx_ctx* c) {
+  if (!c) return FX_OK;
+  if (c->sync) (void)hipFree(c->sync);
+  if (c->timing) (void)hipFree(c->timing);
+  if (c->d_stages) (void)hipFree(c->d_stages);
+  if (c->d_epi) (void)hipFree(c->d_epi);
+  delete c;
+  return FX_OK;
+}
+
+int fx_device_info(fx_ctx* c, int32_t* cus, int32_t* xcds, int32_t* workers, int32_t* lds_bytes) {
+  if (!c) return FX_E_ARG;
+  if (cus) *cus = c->cus;
+  if (xcds) *xcds = FX_XCDS;
+  if (workers) *workers = FX_WORKERS;
+  if (lds_bytes) *lds_bytes = FX_LDS_BYTES;
+  return FX_OK;
+}
+
+int fx_malloc(fx_ctx* c, size_t n, void** p) {
+  if (!p) return fail(c, FX_E_ARG, "null out pointer");
+  HIPCHK(c, hipMalloc(p, n ? n : 16));
+  return FX_OK;
+}
+int fx_free(fx_ctx* c, void* p) {
+  HIPCHK(c, hipFree(p));
+  return FX_OK;
+}
+int fx_memcpy_htod(fx_ctx* c, void* dst, const void* src, size_t n) {
+  HIPCHK(c, hipMemcpy(dst, src, n, hipMemcpyHostToDevice));
+  return FX_OK;
+}
+int fx_memcpy_dtoh(fx_ctx* c, void* dst, const void* src, size_t n) {
+  HIPCHK(c, hipMemcpy(dst, src, n, hipMemcpyDeviceToHost));
+  return FX_OK;
+}
+int fx_memcpy_dtod(fx_ctx* c, void* dst, const void* src, size_t n) {
+  HIPCHK(c, hipMemcpy(dst, src, n, hipMemcpyDeviceToDevice));
+  return FX_OK;
+}
+int fx_memset(fx_ctx* c, void* dst, int v, size_t n) {
+  HIPCHK(c, hipMemset(dst, v, n));
+  return FX_OK;
+}
+int fx_synchronize(fx_ctx* c) {
+  HIPCHK(c, hipDeviceSynchronize());
+  return FX_OK;
+}
+
+// host-side checks of one stage against what its device code assumes
+static int check_stage(fx_ctx* c, const fx_stage& s, int idx) {
+  auto bad = [&](const std::string& m) { return fail(c, FX_E_ARG, "stage " + std::to_string(idx) + ": " + m); };
+  if (s.sync < FX_SYNC_NONE || s.sync > FX_SYNC_GLOBAL) return bad("sync kind");
+  switch (s.op) {
+    case FX_OP_GEMV: {
+      if (!s.w || !s.out || s.n_rows <= 0 || s.k <= 0 || s.k % 8) return bad("gemv shape/pointers");
+      const int nj = (s.k / 8 + 63) / 64;
+      if (!(nj <= 4 || nj == 22)) return bad("gemv K not supported: " + std::to_string(s.k));
+      if (s.k > 11264) return bad("gemv K exceeds LDS row");
+      if (s.in_kind == FX_IN_VEC && !s.x) return bad("gemv input");
+      if (s.in_kind == FX_IN_EMBED && (!s.aux[0] || !s.aux[3])) return bad("embed table / amax");
+      if (s.in_kind == FX_IN_COMBINE && (!s.x || !s.aux[0] || !s.aux[1] || s.n_slots <= 0 || s.n_slots > 16))
+        return bad("combine inputs");
+      if ((s.flags & FX_F_NORM) && !s.w_norm) return bad("norm weight");
+      if ((s.flags & FX_F_RESIDUAL) && !s.res) return bad("residual");
+      if ((s.flags & FX_F_WRITE_X) && !s.aux[2]) return bad("x_out");
+      if ((s.flags & FX_F_ARGMAX) && !s.aux[3]) return bad("amax");
+      break;
+    }
+    case FX_OP_MLA_PREP:
+    case FX_OP_MLA_ATTEND:
+    case FX_OP_MLA_MERGE_UV:
+      if (s.n_rows != 16 || s.d_c != 512 || s.d_r != 64 || s.d_n != 128) return bad("MLA dims must be 16 x (512, 64, 128)");
+      if (!s.x || !s.out || (s.op != FX_OP_MLA_ATTEND && !s.w)) return bad("MLA pointers");
+      if (s.op == FX_OP_MLA_PREP && (!s.aux[0] || !s.aux[1] || !s.aux[2] || !s.aux[3] || !s.aux[4] || !s.w_norm))
+        return bad("prep pointers");
+      if (s.op == FX_OP_MLA_ATTEND) {
+        if (!s.aux[0] || !s.aux[1] || !s.aux[2] || !s.aux[4]) return bad("attend pointers");
+        if (s.split <= 0 || s.n_splits <= 0 || s.prow < s.d_c + 1) return bad("attend splits");
+        if (s.n_splits * s.split < s.s_max) return bad("splits do not cover s_max");
+        if (2 * s.n_splits * 4 > 37 * 1024) return bad("too many splits for the merge table");
+      }
+      break;
+    case FX_OP_MOE_ROUTER:
+      if (!s.w || !s.x || !s.out || !s.w_norm || s.n_rows > 64 || s.k != 2048) return bad("router");
+      break;
+    case FX_OP_MOE_W13:
+      if (!s.w || !s.x || !s.out || !s.w_norm || !s.aux[0] || !s.aux[1] || !s.aux[2] || !s.aux[3] || !s.aux[4] ||
+          !s.aux[7])
+        return bad("w13 pointers");
+      if (s.n_slots != FX_XCDS || s.topk + s.n_forced != s.n_slots || s.aux_i0 > 64 || s.k != 2048) return bad("w13 shape");
+      break;
+    case FX_OP_MOE_W2:
+      if (!s.w || !s.x || !s.out || !s.aux[7] || (s.k / 8 + 63) / 64 > 3) return bad("w2");
+      break;
+    case FX_OP_MOE_COMBINE:
+      if (!s.x || !s.out || !s.aux[0] || !s.aux[1] || s.n_rows % 8) return bad("combine");
+      break;
+    case FX_OP_DENSE_GU:
+      if (!s.w || !s.x || !s.out || !s.w_norm || s.k != 2048) return bad("dense gate/up");
+      break;
+    case FX_OP_ARGMAX:
+      if (!s.aux[3]) return bad("argmax");
+      break;
+    default:
+      return bad("unknown op " + std::to_string(s.op));
+  }
+  return FX_OK;
+}
+
+int fx_load_plan(fx_ctx* c, const fx_stage* st, int32_t n, const fx_stage* epi, int32_t n_epi) {
+  if (!c) return FX_E_ARG;
+  if (n <= 0 || !st) return fail(c, FX_E_ARG, "empty plan");
+  for (int i = 0; i < n; ++i) {
+    int r = check_stage(c, st[i], i);
+    if (r) return r;
+  }
+  for (int i = 0; i < n_epi; ++i) {
+    int r = check_stage(c, epi[i], n + i);
+    if (r) return r;
+  }
+  if (c->d_stages) { HIPCHK(c, hipFree(c->d_stages)); c->d_stages = nullptr; }
+  if (c->d_epi) { HIPCHK(c, hipFree(c->d_epi)); c->d_epi = nullptr; }
+  HIPCHK(c, hipMalloc(&c->d_stages, sizeof(fx_stage) * n));
+  HIPCHK(c, hipMemcpy(c->d_stages, st, sizeof(fx_stage) * n, hipMemcpyHostToDevice));
+  if (n_epi > 0) {
+    HIPCHK(c, hipMalloc(&c->d_epi, sizeof(fx_stage) * n_epi));
+    HIPCHK(c, hipMemcpy(c->d_epi, epi, sizeof(fx_stage) * n_epi, hipMemcpyHostToDevice));
+  }
+  c->n_stages = n;
+  c->n_epi = n_epi;
+  c->h_stages.assign(st, st + n);
+  c->h_epi.assign(epi ? epi : st, epi ? epi + n_epi : st);
+  return FX_OK;
+}
+
+int fx_run(fx_ctx* c, int32_t iters, int32_t step0, int32_t n_prompt, int64_t* tokens, void* stream) {
+  if (!c) return FX_E_ARG;
+  if (!c->d_stages) return fail(c, FX_E_STATE, "no plan loaded");
+  if (iters <= 0 || step0 < 0 || !tokens) return fail(c, FX_E_ARG, "iters/step0/tokens");
+  for (const fx_stage& s : c->h_stages) {
+    if (s.s_max > 0 && step0 + iters > s.s_max) return fail(c, FX_E_ARG, "steps exceed the cache length s_max");
+  }
+  if (c->timing_cap < iters + 1) {
+    if (c->timing) HIPCHK(c, hipFree(c->timing));
+    c->timing_cap = iters + 1;
+    HIPCHK(c, hipMalloc(&c->timing, sizeof(uint64_t) * c->timing_cap));
+  }
+  int syncs = 0;
+  for (const fx_stage& s : c->h_stages) syncs += s.sync != FX_SYNC_NONE;
+  int syncs_epi = 0;
+  for (const fx_stage& s : c->h_epi) syncs_epi += s.sync != FX_SYNC_NONE;
+  const uint64_t total = (uint64_t)syncs * iters + syncs_epi;
+  if ((uint64_t)c->epoch + total > 0xF0000000ull) {
+    HIPCHK(c, hipMemset(c->sync, 0, FX_SYNC_WORDS * 4));
+    c->epoch = 0;
+  }
+  uint32_t err = 0;
+  HIPCHK(c, hipMemcpy(&err, c->sync + FX_FLAG_ERROR, 4, hipMemcpyDeviceToHost));
+  if (err) return fail(c, FX_E_STATE, "a previous run timed out; create a new context");
+  FxRunArgs a;
+  a.stages = c->d_stages;
+  a.n_stages = c->n_stages;
+  a.epi = c->d_epi;
+  a.n_epi = c->n_epi;
+  a.iters = iters;
+  a.step0 = step0;
+  a.n_prompt = n_prompt;
+  a.tokens = tokens;
+  a.sync = c->sync;
+  a.timing = c->timing;
+  a.epoch0 = c->epoch;
+  void* args[] = {&a};
+  hipStream_t s = (hipStream_t)stream;
+  HIPCHK(c, hipLaunchCooperativeKernel((const void*)fx_persistent, dim3(FX_BLOCKS), dim3(FX_THREADS), args, FX_LDS_BYTES, s));
+  c->epoch += (uint32_t)total;
+  c->last_iters = iters;
+  HIPCHK(c, hipStreamSynchronize(s));
+  HIPCHK(c, hipMemcpy(&err, c->sync + FX_FLAG_ERROR, 4, hipMemcpyDeviceToHost));
+  if (err) return fail(c, FX_E_STATE, "a synchronisation wait timed out inside the persistent kernel");
+  return FX_OK;
+}
+
+int fx_read_timing(fx_ctx* c, uint64_t* buf, int32_t n) {
+  if (!c || !buf) return -1;
+  if (!c->timing) return 0;
+  int m = c->last_iters + 1;
+  if (n < m) m = n;
+  if (hipMemcpy(buf, c->timing, sizeof(uint64_t) * m, hipMemcpyDeviceToHost) != hipSuccess) return -1;
+  return m;
+}
+
+int fx_run_stage(fx_ctx* c, const fx_stage* st, int32_t step, int32_t iter, void* stream) {
+  if (!c || !st) return FX_E_ARG;
+  int r = check_stage(c, *st, 0);
+  if (r) return r;
+  hipStream_t s = (hipStream_t)stream;
+  // the embed prologue reads tokens[step]; the argmax reduce always stores tokens[step + 1]
+  const int n_prompt = st->op == FX_OP_ARGMAX ? 0 : (1 << 30);
+  hipLaunchKernelGGL(fx_stage_kernel, dim3(FX_BLOCKS), dim3(FX_THREADS), FX_LDS_BYTES, s, *st, step, iter, n_prompt,
+                     (int64_t*)st->aux[4], c->sync);
+  HIPCHK(c, hipGetLastError());
+  HIPCHK(c, hipStreamSynchronize(s));
+  return FX_OK;
+}
+
+int fx_gen_normal_bf16(fx_ctx* c, void* dst, uint64_t rows, uint64_t row_len, uint64_t dst_stride, uint64_t src_offset,
+                       uint64_t src_stride, uint64_t seed, uint32_t stream, float scale) {
+  if (!dst) return fail(c, FX_E_ARG, "null dst");
+  if (rows == 0 || row_len == 0) return FX_OK;
+  if (rows == 1 || (dst_stride == row_len && src_stride == row_len)) {
+    const uint64_t n = rows * row_len;
+    uint64_t blocks = (n + 3) / 4 + 1;
+    uint64_t grid = (blocks + 255) / 256;
+    if (grid > 65536) grid = 65536;
+    hipLaunchKernelGGL(fx_gen_kernel, dim3((unsigned)grid), dim3(256), 0, 0, (uint16_t*)dst, n, seed, stream, scale,
+                       src_offset);
+  } else {
+    uint64_t grid = (rows * row_len + 255) / 256;
+    if (grid > 65536) grid = 65536;
+    hipLaunchKernelGGL(fx_gen2d_kernel, dim3((unsigned)grid), dim3(256), 0, 0, (uint16_t*)dst, rows, row_len, dst_stride,
+                       src_offset, src_stride, seed, stream, scale);
+  }
+  HIPCHK(c, hipGetLastError());
+  return FX_OK;
+}
+
+int fx_fill_u16(fx_ctx* c, void* dst, uint64_t n, uint16_t v) {
+  if (!dst) return fail(c, FX_E_ARG, "null dst");
+  if (n == 0) return FX_OK;
+  uint64_t grid = (n + 255) / 256;
+  if (grid > 65536) grid = 65536;
+  hipLaunchKernelGGL(fx_fill_kernel, dim3((unsigned)grid), dim3(256), 0, 0, (uint16_t*)dst, n, v);
+  HIPCHK(c, hipGetLastError());
+  return FX_OK;
+}
+
+}  // extern "C"

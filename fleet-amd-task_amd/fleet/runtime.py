@@ -1,0 +1,228 @@
+"""ctypes binding of libfleet_mi355x.so (include/fleet_mi355x.h).
+
+The host side of the drop-in boundary: device buffers, the task-table entry (fx_stage) and the
+calls that replace the mirage runtime's PersistentKernel / compile / run (fleet/build_graph.py:561-593,
+harness/run_fleet.py:551-593 in the reference). No torch: device memory comes from the library's
+own hipMalloc wrapper, so the same process can run under rocprofv3.
+
+The library must be built (fleet-amd-task_amd/csrc/Makefile, or __graft_entry__.build()); a missing
+library or a non-gfx950 device raises FxError, there is no fallback.
+"""
+import ctypes
+import os
+from pathlib import Path
+
+import numpy as np
+
+PKG = Path(__file__).resolve().parent.parent
+LIB_PATH = Path(os.environ.get("FX_LIB", PKG / "lib" / "libfleet_mi355x.so"))
+
+FX_OP_GEMV, FX_OP_MLA_PREP, FX_OP_MLA_ATTEND, FX_OP_MLA_MERGE_UV = 1, 2, 3, 4
+FX_OP_MOE_ROUTER, FX_OP_MOE_W13, FX_OP_MOE_W2, FX_OP_MOE_COMBINE = 5, 6, 7, 8
+FX_OP_DENSE_GU, FX_OP_ARGMAX = 9, 10
+FX_IN_VEC, FX_IN_EMBED, FX_IN_COMBINE = 0, 1, 2
+FX_F_NORM, FX_F_RESIDUAL, FX_F_WRITE_X, FX_F_ARGMAX, FX_F_HEAD = 1, 2, 4, 8, 16
+FX_SYNC_NONE, FX_SYNC_XCD, FX_SYNC_GLOBAL = 0, 1, 2
+WORKERS = 248          # 256 CUs minus one scheduler workgroup per XCD
+XCDS = 8
+
+
+class FxError(RuntimeError):
+    pass
+
+
+class FxStage(ctypes.Structure):
+    """Mirror of struct fx_stage (include/fleet_mi355x.h)."""
+    _fields_ = [(n, ctypes.c_int32) for n in (
+        "op", "sync", "flags", "in_kind", "layer", "n_rows", "k", "n_slots", "topk", "n_forced", "split", "n_splits",
+        "d_c", "d_r", "d_n", "prow", "s_scores", "s_max", "aux_i0", "aux_i1")] + \
+        [(n, ctypes.c_float) for n in ("eps", "scale", "scaling", "aux_f")] + \
+        [(n, ctypes.c_uint64) for n in ("w", "x", "w_norm", "res", "out")] + [("aux", ctypes.c_uint64 * 8)]
+
+    def set(self, **kw):
+        for k, v in kw.items():
+            if k == "aux":
+                for i, p in v.items():
+                    self.aux[i] = int(p or 0)
+            else:
+                setattr(self, k, v if not isinstance(v, DeviceBuffer) else v.ptr)
+        return self
+
+    def to_dict(self):
+        d = {n: getattr(self, n) for n, _ in self._fields_ if n != "aux"}
+        d["aux"] = list(self.aux)
+        return d
+
+
+assert ctypes.sizeof(FxStage) == 200, ctypes.sizeof(FxStage)   # static_assert in fx_runtime.hip
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        raise FxError(f"{LIB_PATH} is missing: build it with `make -C fleet-amd-task_amd/csrc` "
+                      f"or __graft_entry__.build()")
+    L = ctypes.CDLL(str(LIB_PATH))
+    vp, i32, u64, sz = ctypes.c_void_p, ctypes.c_int32, ctypes.c_uint64, ctypes.c_size_t
+    sig = {
+        "fx_abi_version": (ctypes.c_int, []),
+        "fx_create": (ctypes.c_int, [ctypes.c_int, ctypes.POINTER(vp)]),
+        "fx_destroy": (ctypes.c_int, [vp]),
+        "fx_last_error": (ctypes.c_char_p, [vp]),
+        "fx_device_info": (ctypes.c_int, [vp, ctypes.POINTER(i32), ctypes.POINTER(i32), ctypes.POINTER(i32),
+                                          ctypes.POINTER(i32)]),
+        "fx_malloc": (ctypes.c_int, [vp, sz, ctypes.POINTER(vp)]),
+        "fx_free": (ctypes.c_int, [vp, vp]),
+        "fx_memcpy_htod": (ctypes.c_int, [vp, vp, vp, sz]),
+        "fx_memcpy_dtoh": (ctypes.c_int, [vp, vp, vp, sz]),
+        "fx_memcpy_dtod": (ctypes.c_int, [vp, vp, vp, sz]),
+        "fx_memset": (ctypes.c_int, [vp, vp, ctypes.c_int, sz]),
+        "fx_synchronize": (ctypes.c_int, [vp]),
+        "fx_load_plan": (ctypes.c_int, [vp, ctypes.POINTER(FxStage), i32, ctypes.POINTER(FxStage), i32]),
+        "fx_run": (ctypes.c_int, [vp, i32, i32, i32, vp, vp]),
+        "fx_read_timing": (ctypes.c_int, [vp, ctypes.POINTER(ctypes.c_uint64), i32]),
+        "fx_run_stage": (ctypes.c_int, [vp, ctypes.POINTER(FxStage), i32, i32, vp]),
+        "fx_gen_normal_bf16": (ctypes.c_int, [vp, vp, u64, u64, u64, u64, u64, u64, ctypes.c_uint32, ctypes.c_float]),
+        "fx_fill_u16": (ctypes.c_int, [vp, vp, u64, ctypes.c_uint16]),
+    }
+    for name, (res, args) in sig.items():
+        f = getattr(L, name)
+        f.restype = res
+        f.argtypes = args
+    _lib = L
+    return L
+
+
+EXPORTS = ("fx_abi_version", "fx_create", "fx_destroy", "fx_last_error", "fx_device_info", "fx_malloc", "fx_free",
+           "fx_memcpy_htod", "fx_memcpy_dtoh", "fx_memcpy_dtod", "fx_memset", "fx_synchronize", "fx_load_plan",
+           "fx_run", "fx_read_timing", "fx_run_stage", "fx_gen_normal_bf16", "fx_fill_u16")
+
+
+class Runtime:
+    """One device context (fx_create). Owns nothing of the model; buffers are DeviceBuffer objects."""
+
+    def __init__(self, device=0):
+        self.L = lib()
+        h = ctypes.c_void_p()
+        rc = self.L.fx_create(device, ctypes.byref(h))
+        self.h = h
+        if rc:
+            msg = self.L.fx_last_error(h).decode() if h.value else f"fx_create failed ({rc})"
+            raise FxError(msg)
+        self._bufs = []
+
+    def check(self, rc, what=""):
+        if rc:
+            raise FxError(f"{what}: {self.L.fx_last_error(self.h).decode()} (code {rc})")
+
+    def info(self):
+        v = [ctypes.c_int32() for _ in range(4)]
+        self.check(self.L.fx_device_info(self.h, *[ctypes.byref(x) for x in v]), "fx_device_info")
+        return dict(zip(("cus", "xcds", "workers", "lds_bytes"), [x.value for x in v]))
+
+    def alloc(self, shape, dtype):
+        return DeviceBuffer(self, shape, dtype)
+
+    def synchronize(self):
+        self.check(self.L.fx_synchronize(self.h), "fx_synchronize")
+
+    def gen_normal_bf16(self, buf, n, seed, stream, scale, dst_offset=0, src_offset=0, rows=1, row_len=None,
+                        dst_stride=None, src_stride=None):
+        """buf[dst_offset + r*dst_stride + j] = bf16(scale * N(seed, stream, src_offset + r*src_stride + j))."""
+        row_len = n if row_len is None else row_len
+        dst_stride = row_len if dst_stride is None else dst_stride
+        src_stride = row_len if src_stride is None else src_stride
+        ptr = buf.ptr + 2 * dst_offset
+        self.check(self.L.fx_gen_normal_bf16(self.h, ptr, rows, row_len, dst_stride, src_offset, src_stride, seed,
+                                             stream, scale), "fx_gen_normal_bf16")
+
+    def fill_u16(self, buf, value, n=None, offset=0):
+        n = buf.nbytes // 2 - offset if n is None else n
+        self.check(self.L.fx_fill_u16(self.h, buf.ptr + 2 * offset, n, value), "fx_fill_u16")
+
+    def load_plan(self, stages, epilogue=()):
+        arr = (FxStage * len(stages))(*stages)
+        epi = (FxStage * max(1, len(epilogue)))(*epilogue) if epilogue else None
+        self.check(self.L.fx_load_plan(self.h, arr, len(stages), epi, len(epilogue)), "fx_load_plan")
+
+    def run(self, iters, step0, n_prompt, tokens):
+        self.check(self.L.fx_run(self.h, iters, step0, n_prompt, tokens.ptr, None), "fx_run")
+
+    def timing(self, n):
+        buf = (ctypes.c_uint64 * (n + 1))()
+        m = self.L.fx_read_timing(self.h, buf, n + 1)
+        return np.array(buf[:max(m, 0)], np.uint64)
+
+    def run_stage(self, stage, step=0, it=0):
+        self.check(self.L.fx_run_stage(self.h, ctypes.byref(stage), step, it, None), "fx_run_stage")
+
+    def close(self):
+        if self.h:
+            self.L.fx_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+_DT = {"bf16": np.uint16, "f32": np.float32, "i32": np.int32, "i64": np.int64, "u16": np.uint16, "u8": np.uint8}
+
+
+class DeviceBuffer:
+    """A device allocation with a shape and a dtype name (bf16 kept as uint16 bit patterns)."""
+
+    def __init__(self, rt, shape, dtype):
+        self.rt = rt
+        self.shape = tuple(int(s) for s in (shape if isinstance(shape, (tuple, list)) else (shape,)))
+        self.dtype = dtype
+        self.np_dtype = _DT[dtype]
+        self.nbytes = int(np.prod(self.shape, dtype=np.int64)) * np.dtype(self.np_dtype).itemsize
+        p = ctypes.c_void_p()
+        rt.check(rt.L.fx_malloc(rt.h, max(self.nbytes, 16), ctypes.byref(p)), "fx_malloc")
+        self.ptr = p.value
+
+    def upload(self, arr):
+        a = np.ascontiguousarray(arr, dtype=self.np_dtype)
+        assert a.nbytes == self.nbytes, (a.shape, self.shape)
+        self.rt.check(self.rt.L.fx_memcpy_htod(self.rt.h, self.ptr, a.ctypes.data, a.nbytes), "htod")
+        return self
+
+    def upload_at(self, arr, elem_offset):
+        a = np.ascontiguousarray(arr, dtype=self.np_dtype)
+        it = np.dtype(self.np_dtype).itemsize
+        assert elem_offset * it + a.nbytes <= self.nbytes
+        self.rt.check(self.rt.L.fx_memcpy_htod(self.rt.h, self.ptr + elem_offset * it, a.ctypes.data, a.nbytes), "htod")
+
+    def download(self):
+        out = np.empty(self.shape, self.np_dtype)
+        self.rt.check(self.rt.L.fx_memcpy_dtoh(self.rt.h, out.ctypes.data, self.ptr, self.nbytes), "dtoh")
+        return out
+
+    def download_range(self, elem_offset, n):
+        it = np.dtype(self.np_dtype).itemsize
+        out = np.empty(n, self.np_dtype)
+        self.rt.check(self.rt.L.fx_memcpy_dtoh(self.rt.h, out.ctypes.data, self.ptr + elem_offset * it, n * it), "dtoh")
+        return out
+
+    def zero(self):
+        self.rt.check(self.rt.L.fx_memset(self.rt.h, self.ptr, 0, self.nbytes), "memset")
+        return self
+
+    def free(self):
+        if self.ptr:
+            self.rt.L.fx_free(self.rt.h, self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            if self.ptr and self.rt.h:
+                self.free()
+        except Exception:
+            pass

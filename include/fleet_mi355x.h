@@ -1,0 +1,171 @@
+/* fleet_mi355x.h - C ABI of the MI355X (gfx950) batch-1 DeepSeek-V2-Lite decode path.
+ *
+ * The reference drives its decode through a Python plan -> mirage runtime boundary:
+ *   mi.PersistentKernel(...), mpk.attach_input / mpk.<op>_layer / kn_graph.register_task,
+ *   mpk.compile(), mpk()                          (fleet/build_graph.py:36-46, 478-528, 561-593;
+ *                                                  harness/run_fleet.py:551-593)
+ * and a per-kernel launcher for its kernel suite (fleet/tasks/kernel_tests_mi300.cu:1-47).
+ * This header is that boundary as a C ABI: plain pointers and sizes, no torch types. The host
+ * (fleet/build_graph.py's counterpart, through ctypes) owns every device buffer of the model and
+ * hands raw device pointers in a task table (the plan's calls, one fx_stage each); the library
+ * owns only its synchronisation flags and timing slots.
+ *
+ * Errors: every entry returns 0 on success or a nonzero FX_E_* code; fx_last_error() returns the
+ * message of the last failure on that context (mirrors the suite's exit codes,
+ * kernel_tests_mi300.cu:46-47, and the plan asserts run before launch, harness/run_fleet.py:507-513).
+ * Threading: one host thread per context; fx_run returns after every iteration has finished, as
+ * mpk() does (harness/run_fleet.py:590-593).
+ */
+#ifndef FLEET_MI355X_H
+#define FLEET_MI355X_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FX_ABI_VERSION 1
+
+/* ---- error codes ---------------------------------------------------------------------------- */
+#define FX_OK 0
+#define FX_E_HIP 1         /* a HIP runtime call failed */
+#define FX_E_ARG 2         /* an argument or a plan entry is invalid (checked before launch) */
+#define FX_E_DEVICE 3      /* the device is not a gfx950 with the expected layout */
+#define FX_E_STATE 4       /* call out of order (no plan loaded, ...) */
+
+/* ---- operators of the task table --------------------------------------------------------------
+ * One per plan call (fleet/graph_plan.py OUTPUT_ARGS names in brackets). Pointer fields of
+ * fx_stage used by each op are listed with it; every device pointer is a bf16 (uint16) array
+ * unless marked f32 / i32 / i64. */
+enum fx_op {
+  /* [linear_gemv_layer] out[n] = bf16(dot(w[n], xin) (+ res[n])) for n < n_rows; K = k.
+   * Input xin by in_kind: FX_IN_VEC x; FX_IN_EMBED w_embed(aux0)[token]; FX_IN_COMBINE
+   * bf16(x + sum_s out8(aux0)[s] * topk_w(aux1 f32)[s]). FX_F_NORM: xin := rmsnorm(xin, w_norm).
+   * FX_F_WRITE_X: worker 0 also stores the prologue's row (before the norm) to x_out(aux2).
+   * FX_F_ARGMAX: per-worker (max, index) of the bf16 outputs to amax(aux3 f32[2*workers]).
+   * FX_IN_EMBED reads the token from tokens(aux4 i64)[step] or, at or past n_prompt, reduces
+   * the previous head's amax(aux3) and stores the id to tokens[step]. */
+  FX_OP_GEMV = 1,
+  /* [mla_prep_layer] qkva(x) -> c_kv(aux0)[step], k_pe(aux1)[step] (cache rows), ql_nope(out)
+   * [nh, d_c], q_pe(aux2) [nh, d_r]; w = W_uk [nh, d_n, d_c]; w_norm = kv_a_layernorm weight;
+   * cos(aux3), sin(aux4) [s_max, d_r]. Heads nh/8 per XCD. */
+  FX_OP_MLA_PREP = 2,
+  /* [mla_attend_layer] ql_nope(x), q_pe(aux2), c_kv(aux0), k_pe(aux1) -> partials(out f32)
+   * [n_splits, nh, prow]; optional scores(aux3 f32) [nh, s_scores]; the last split task of each
+   * XCD merges its heads' live splits into o_merged(aux4) [nh, d_c] (bf16). */
+  FX_OP_MLA_ATTEND = 3,
+  /* [mla_merge_uv_layer] attn(out)[h*d_v+v] = bf16(dot(o_merged(x)[h], W_uv(w)[h][v])), d_v in
+   * the d_n field; the LSE merge of the partials into o_merged ran at the end of MLA_ATTEND. */
+  FX_OP_MLA_MERGE_UV = 4,
+  /* [moe_router_layer] h = rmsnorm(x_res(x), w_norm); logits_x(out f32)[xcd][e] = dot(W_gate(w)[e], h)
+   * computed by every XCD for its own use (XCDs whose slot is a forced expert skip it). */
+  FX_OP_MOE_ROUTER = 5,
+  /* [gang_moe_w13_gemv_layer] softmax/top-k of logits_x(aux0 f32)[xcd], slot xcd's expert e;
+   * act8(out)[slot][i] = bf16(silu(bf16(W13(w)[e][i] h)) * bf16(W13[e][I+i] h)), h recomputed
+   * from x_res(x) and w_norm. Worker 0 of XCD 0 stores topk_w(aux1 f32), routing(aux2 i32),
+   * mask(aux3 i32), logits(aux4 f32), h(aux6) and route_log(aux5 i32 [prow][aux_i1][n_slots]) at
+   * row step - (n_prompt - 1) when that row is in [0, prow); rank 0 of each XCD stores its slot's
+   * expert id to sel(aux7 i32 [8]); aux_i0 = E. */
+  FX_OP_MOE_W13 = 6,
+  /* [gang_moe_w2_linear_layer] out8(out)[slot][n] = bf16(dot(W2(w)[e][n], act8(x)[slot])),
+   * e = sel(aux7)[slot]. */
+  FX_OP_MOE_W2 = 7,
+  /* [moe_mul_sum_add_layer] x_res(out) = bf16(x_res(x) + sum_s out8(aux0)[s] * topk_w(aux1 f32)[s]). */
+  FX_OP_MOE_COMBINE = 8,
+  /* [gang_linear_silu_layer] h = rmsnorm(x_res(x), w_norm); act(out)[i] = bf16(silu(bf16(w[i] h)) *
+   * bf16(w[I+i] h)) for i < n_rows (= I); h to aux6 when non-NULL. */
+  FX_OP_DENSE_GU = 9,
+  /* [argmax_reduce_layer] tokens(aux4 i64)[step + 1] = argmax from amax(aux3). */
+  FX_OP_ARGMAX = 10,
+};
+
+/* GEMV input kinds */
+#define FX_IN_VEC 0
+#define FX_IN_EMBED 1
+#define FX_IN_COMBINE 2
+
+/* flags */
+#define FX_F_NORM 1u
+#define FX_F_RESIDUAL 2u
+#define FX_F_WRITE_X 4u
+#define FX_F_ARGMAX 8u
+#define FX_F_HEAD 16u      /* the stage belongs to the head: skipped while step + 1 < n_prompt */
+
+/* synchronisation after a stage */
+#define FX_SYNC_NONE 0
+#define FX_SYNC_XCD 1      /* the 31 workers of each XCD, through that XCD's scheduler */
+#define FX_SYNC_GLOBAL 2   /* every worker of the device */
+
+/* One entry of the task table: one operator of the plan (fleet/graph_plan.py Call). */
+typedef struct fx_stage {
+  int32_t op, sync, flags, in_kind;
+  int32_t layer;      /* decoder layer (route_log row: layer - 1), -1 outside the layers */
+  int32_t n_rows;     /* GEMV/DENSE_GU rows; heads for MLA ops; E for the router */
+  int32_t k;          /* reduction width (H, or I for W2 / down) */
+  int32_t n_slots;    /* MoE slots: topk + forced (8) */
+  int32_t topk, n_forced, split, n_splits;
+  int32_t d_c, d_r, d_n, prow;
+  int32_t s_scores, s_max, aux_i0, aux_i1;
+  float eps, scale, scaling, aux_f;
+  uint64_t w, x, w_norm, res, out;
+  uint64_t aux[8];
+} fx_stage;
+
+/* ---- context ---------------------------------------------------------------------------------- */
+typedef struct fx_ctx fx_ctx;
+
+/* Replaces mi.PersistentKernel(...) (fleet/build_graph.py:583-589): binds a device, checks it is a
+ * gfx950 with 8 XCDs, allocates the synchronisation flags. */
+int fx_create(int device, fx_ctx** out);
+int fx_destroy(fx_ctx* ctx);
+const char* fx_last_error(fx_ctx* ctx);
+int fx_abi_version(void);
+
+/* Device facts: CUs, XCDs, workers (CUs minus one scheduler per XCD), LDS per workgroup. */
+int fx_device_info(fx_ctx* ctx, int32_t* cus, int32_t* xcds, int32_t* workers, int32_t* lds_bytes);
+
+/* ---- memory (for hosts without torch: the ctypes runtime allocates through these) ------------- */
+int fx_malloc(fx_ctx* ctx, size_t nbytes, void** dptr);
+int fx_free(fx_ctx* ctx, void* dptr);
+int fx_memcpy_htod(fx_ctx* ctx, void* dst, const void* src, size_t nbytes);
+int fx_memcpy_dtoh(fx_ctx* ctx, void* dst, const void* src, size_t nbytes);
+int fx_memcpy_dtod(fx_ctx* ctx, void* dst, const void* src, size_t nbytes);
+int fx_memset(fx_ctx* ctx, void* dst, int value, size_t nbytes);
+int fx_synchronize(fx_ctx* ctx);
+
+/* ---- plan and run ----------------------------------------------------------------------------- */
+/* Replaces mpk.compile() (the codegen + JIT of the worker switch, harness/run_fleet.py:556): the
+ * task table is validated on the host (shapes, pointer presence, sync kinds) and uploaded. */
+int fx_load_plan(fx_ctx* ctx, const fx_stage* stages, int32_t n_stages, const fx_stage* epilogue,
+                 int32_t n_epilogue);
+
+/* Replaces mpk() (harness/run_fleet.py:590-593): one persistent launch that runs `iters` decode
+ * iterations at positions step0 .. step0 + iters - 1. tokens (int64 [>= step0 + iters + 1]) holds the
+ * prompt in [0, n_prompt); iteration i reads tokens[step0 + i] and, when step0 + i + 1 >= n_prompt,
+ * the head's argmax is stored to tokens[step0 + i + 1]. stream: a hipStream_t or NULL. */
+int fx_run(fx_ctx* ctx, int32_t iters, int32_t step0, int32_t n_prompt, int64_t* tokens, void* stream);
+
+/* Per-iteration timestamps of the last fx_run (s_memrealtime, 100 MHz): buf[0] at the start of
+ * iteration 0, buf[i] at the start of iteration i, buf[iters] at the end. Replaces the [FWD_PASS]
+ * lines and event_timing.json (harness/measure.py:187-190). Returns the count written. */
+int fx_read_timing(fx_ctx* ctx, uint64_t* buf, int32_t n);
+
+/* Kernel-suite entry (kernel_tests_mi300.cu counterpart): one stage as a standalone launch of all
+ * workers, with the same task split as inside fx_run; step is the decode position. */
+int fx_run_stage(fx_ctx* ctx, const fx_stage* stage, int32_t step, int32_t iter, void* stream);
+
+/* ---- seeded inputs (pack_weights counterpart: fills the packed keys from a seed) -------------- */
+/* dst[r * dst_stride + j] = bf16(scale * z(src_offset + r * src_stride + j)) for r < rows, j < row_len,
+ * where z(i) is element i of the N(0,1) stream: Philox4x32-10 (key = seed, counter = (i / 4, stream,
+ * 0x5EED)) word pairs through Box-Muller, element i % 4 of the block; bit-identical to the CPU
+ * generator. A tensor is one stream; packing it (a row range, a column slice) is a strided call. */
+int fx_gen_normal_bf16(fx_ctx* ctx, void* dst, uint64_t rows, uint64_t row_len, uint64_t dst_stride,
+                       uint64_t src_offset, uint64_t src_stride, uint64_t seed, uint32_t stream, float scale);
+int fx_fill_u16(fx_ctx* ctx, void* dst, uint64_t n, uint16_t value);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* FLEET_MI355X_H */

@@ -1,0 +1,659 @@
+/* CPU oracle for the batch-1 DeepSeek-V2-Lite decode path.
+ *
+ * TEST INFRASTRUCTURE ONLY. This library is the checker the GPU path is compared against; only
+ * tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may load it. The product path
+ * never links or calls it.
+ *
+ * It restates the arithmetic of the reference's numpy specification (harness/numpy_ref.py) with
+ * every FP32 reduction order fixed, so that the GPU kernels, which follow the same fixed orders,
+ * agree with it bit for bit. numpy_ref leaves the order of its matmul/einsum sums to BLAS; that
+ * order is the one thing this restatement chooses (see "spec" below) and the reason its bits can
+ * differ from numpy_ref-as-run by FP32 reassociation (parity of those raw bits is unpinned).
+ *
+ * Spec (all FP32, IEEE round-to-nearest-even, no contraction unless fmaf is written):
+ *   bf16r        round to bf16, RNE                         numpy_ref.py:36-42
+ *   dot_lanes    chunk c (8 contiguous elements) -> lane c % 64, lane sums its chunks in
+ *                increasing c with one fma per element, then an xor butterfly over the
+ *                smallest power of two >= min(64, chunks) lanes, offsets 1, 2, 4, ..., 32.
+ *                bf16 x bf16 products are exact in FP32, so fma == mul + add here.
+ *   exp_s/log_s  range reduction + polynomial, defined below (numpy's exp/log are libm's).
+ *   attention    scores: 4 sequential chains over the latent width + 1 over the rope width;
+ *                softmax sums and the value product: sequential over positions (VALU order).
+ *
+ * Build: oracle/Makefile (gcc -O3 -fopenmp -ffp-contract=off). Python wrapper: oracle/oracle.py.
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+#define SPEC_LANES 64
+#define SPEC_CHUNK 8
+#define ATTN_TILE 32
+
+/* ------------------------------------------------------------------------------------------ */
+/* bf16                                                                                        */
+
+static inline float b2f(uint16_t u) {
+  uint32_t v = (uint32_t)u << 16;
+  float f;
+  memcpy(&f, &v, 4);
+  return f;
+}
+
+/* numpy_ref.py:36-42: u + 0x7FFF + lsb, then truncate. */
+static inline uint16_t f2b(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  uint32_t lsb = (u >> 16) & 1u;
+  u = u + 0x7FFFu + lsb;
+  return (uint16_t)(u >> 16);
+}
+
+static inline float bf16r(float f) { return b2f(f2b(f)); }
+
+uint16_t or_f32_to_bf16(float f) { return f2b(f); }
+float or_bf16_to_f32(uint16_t u) { return b2f(u); }
+
+void or_round_bf16_array(const float* x, uint16_t* y, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) y[i] = f2b(x[i]);
+}
+
+/* ------------------------------------------------------------------------------------------ */
+/* exp / log / silu of the spec                                                                */
+
+static inline float fbits(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+static inline uint32_t ubits(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+
+/* exp: x < -87 -> 0 (also -inf), x > 88 -> +inf; else n = rint(x*log2e), Cody-Waite r,
+ * degree-6 Taylor in Horner form with separate mul and add, times 2^n built from bits. */
+float or_exp(float x) {
+  if (!(x >= -87.0f)) return 0.0f; /* -inf and NaN-free inputs only */
+  if (x > 88.0f) return fbits(0x7f800000u);
+  const float LOG2E = 1.44269504088896341f;
+  const float LN2_HI = 0.693145751953125f;       /* 0x3f317200 */
+  const float LN2_LO = 1.42860682030941723e-06f; /* ln2 - LN2_HI */
+  float t = x * LOG2E;
+  float n = rintf(t);
+  float r = x - n * LN2_HI;
+  r = r - n * LN2_LO;
+  float p = 1.3888889e-3f;          /* 1/720 */
+  p = p * r + 8.3333333e-3f;        /* 1/120 */
+  p = p * r + 4.1666668e-2f;        /* 1/24 */
+  p = p * r + 1.6666667e-1f;        /* 1/6 */
+  p = p * r + 0.5f;
+  p = p * r + 1.0f;
+  p = p * r + 1.0f;
+  int ni = (int)n;
+  float scale = fbits((uint32_t)(ni + 127) << 23);
+  return p * scale;
+}
+
+/* log for x > 0 normal: x = 2^e m, m in [sqrt(1/2), sqrt(2)], s = (m-1)/(m+1),
+ * log m = s (2 + z (2/3 + z (2/5 + z (2/7 + z 2/9)))), z = s^2; result = e ln2 + log m. */
+float or_log(float x) {
+  uint32_t u = ubits(x);
+  int e = (int)((u >> 23) & 0xffu) - 127;
+  float m = fbits((u & 0x007fffffu) | 0x3f800000u);
+  if (m > 1.41421356f) { m = m * 0.5f; e = e + 1; }
+  float f = m - 1.0f;
+  float s = f / (2.0f + f);
+  float z = s * s;
+  float p = 0.22222222f;           /* 2/9 */
+  p = p * z + 0.28571429f;         /* 2/7 */
+  p = p * z + 0.4f;                /* 2/5 */
+  p = p * z + 0.66666669f;         /* 2/3 */
+  p = p * z + 2.0f;
+  float lm = s * p;
+  const float LN2 = 0.693147182f;
+  return (float)e * LN2 + lm;
+}
+
+/* numpy_ref.py:248-253: x / (1 + exp(-x)) in FP32 with the spec's exp. */
+float or_silu(float x) { return x / (1.0f + or_exp(-x)); }
+
+/* ------------------------------------------------------------------------------------------ */
+/* dot products of the spec                                                                    */
+
+static inline int lanes_for(int nchunk) {
+  int nl = 1;
+  while (nl < nchunk && nl < SPEC_LANES) nl <<= 1;
+  return nl;
+}
+
+static inline float butterfly(float* acc, int nl) {
+  for (int off = 1; off < nl; off <<= 1) {
+    float tmp[SPEC_LANES];
+    for (int l = 0; l < nl; ++l) tmp[l] = acc[l] + acc[l ^ off];
+    memcpy(acc, tmp, sizeof(float) * nl);
+  }
+  return acc[0];
+}
+
+/* a: bf16 row, b: f32 vector (bf16 values or exact f32), K multiple of 8. */
+static float dot_lanes_bf(const uint16_t* a, const float* b, int K) {
+  int nchunk = K / SPEC_CHUNK;
+  int nl = lanes_for(nchunk);
+  float acc[SPEC_LANES];
+  for (int l = 0; l < nl; ++l) acc[l] = 0.0f;
+  for (int c = 0; c < nchunk; ++c) {
+    int l = c & (SPEC_LANES - 1);
+    float s = acc[l];
+    const uint16_t* ap = a + (size_t)c * SPEC_CHUNK;
+    const float* bp = b + (size_t)c * SPEC_CHUNK;
+    for (int e = 0; e < SPEC_CHUNK; ++e) s = s + b2f(ap[e]) * bp[e];
+    acc[l] = s;
+  }
+  return butterfly(acc, nl);
+}
+
+/* column dot: sum_n a[n] * B[n * ldb] with the lane order over n. */
+static float dot_lanes_col(const float* a, const uint16_t* B, int K, int ldb) {
+  int nchunk = K / SPEC_CHUNK;
+  int nl = lanes_for(nchunk);
+  float acc[SPEC_LANES];
+  for (int l = 0; l < nl; ++l) acc[l] = 0.0f;
+  for (int c = 0; c < nchunk; ++c) {
+    int l = c & (SPEC_LANES - 1);
+    float s = acc[l];
+    for (int e = 0; e < SPEC_CHUNK; ++e) {
+      int n = c * SPEC_CHUNK + e;
+      s = s + a[n] * b2f(B[(size_t)n * ldb]);
+    }
+    acc[l] = s;
+  }
+  return butterfly(acc, nl);
+}
+
+float or_dot_lanes(const uint16_t* a, const uint16_t* b, int K) {
+  float* bf = (float*)malloc(sizeof(float) * K);
+  for (int i = 0; i < K; ++i) bf[i] = b2f(b[i]);
+  float r = dot_lanes_bf(a, bf, K);
+  free(bf);
+  return r;
+}
+
+/* ------------------------------------------------------------------------------------------ */
+/* RMSNorm and RoPE                                                                            */
+
+/* numpy_ref.py:54-60: var = sum(x^2)/D (spec order), xn = bf16(x * (1/sqrt(var+eps))),
+ * y = bf16(w * xn). Returns y as f32 values (bf16-exact) and optionally bf16 bits. */
+static void rmsnorm_f(const uint16_t* x, const uint16_t* w, int D, float eps, float* y) {
+  float* xf = (float*)malloc(sizeof(float) * D);
+  for (int i = 0; i < D; ++i) xf[i] = b2f(x[i]);
+  float ss = dot_lanes_bf(x, xf, D);
+  float var = ss / (float)D;
+  float rs = 1.0f / sqrtf(var + eps);
+  for (int i = 0; i < D; ++i) {
+    float xn = bf16r(xf[i] * rs);
+    y[i] = bf16r(b2f(w[i]) * xn);
+  }
+  free(xf);
+}
+
+void or_rmsnorm(const uint16_t* x, const uint16_t* w, int D, float eps, uint16_t* y) {
+  float* yf = (float*)malloc(sizeof(float) * D);
+  rmsnorm_f(x, w, D, eps, yf);
+  for (int i = 0; i < D; ++i) y[i] = f2b(yf[i]);
+  free(yf);
+}
+
+/* numpy_ref.py:63-71 (HF modeling_deepseek.py:339-371): de-interleave (even, odd) pairs,
+ * out = bf16(bf16(x*cos) + bf16(rotate_half(x)*sin)). d = 64. */
+void or_rope(const uint16_t* x, const uint16_t* cosr, const uint16_t* sinr, int d, uint16_t* y) {
+  float xd[256], rot[256];
+  int h = d / 2;
+  for (int i = 0; i < h; ++i) { xd[i] = b2f(x[2 * i]); xd[h + i] = b2f(x[2 * i + 1]); }
+  for (int i = 0; i < h; ++i) { rot[i] = -xd[h + i]; rot[h + i] = xd[i]; }
+  for (int i = 0; i < d; ++i) {
+    float a = bf16r(xd[i] * b2f(cosr[i]));
+    float b = bf16r(rot[i] * b2f(sinr[i]));
+    y[i] = f2b(a + b);
+  }
+}
+
+/* ------------------------------------------------------------------------------------------ */
+/* linears (numpy_ref.py:295-313)                                                              */
+
+/* out[n] = bf16(dot(W[n], x) (+ res[n])), x given as bf16. norm_w != NULL: x := rmsnorm(x). */
+void or_linear(const uint16_t* W, const uint16_t* x, const uint16_t* norm_w, float eps, const uint16_t* res,
+               int64_t N, int K, uint16_t* out, uint16_t* h_out) {
+  float* xf = (float*)malloc(sizeof(float) * K);
+  if (norm_w) {
+    rmsnorm_f(x, norm_w, K, eps, xf);
+    if (h_out)
+      for (int i = 0; i < K; ++i) h_out[i] = f2b(xf[i]);
+  } else {
+    for (int i = 0; i < K; ++i) xf[i] = b2f(x[i]);
+  }
+#pragma omp parallel for schedule(static)
+  for (int64_t n = 0; n < N; ++n) {
+    float d = dot_lanes_bf(W + (size_t)n * K, xf, K);
+    if (res) d = d + b2f(res[n]);
+    out[n] = f2b(d);
+  }
+  free(xf);
+}
+
+/* f32 logits variant (router): out[n] = dot(W[n], x) unrounded. */
+void or_linear_f32(const uint16_t* W, const uint16_t* x, int64_t N, int K, float* out) {
+  float* xf = (float*)malloc(sizeof(float) * K);
+  for (int i = 0; i < K; ++i) xf[i] = b2f(x[i]);
+#pragma omp parallel for schedule(static)
+  for (int64_t n = 0; n < N; ++n) out[n] = dot_lanes_bf(W + (size_t)n * K, xf, K);
+  free(xf);
+}
+
+/* ------------------------------------------------------------------------------------------ */
+/* MLA prep (numpy_ref.py:85-103)                                                              */
+
+void or_mla_prep(const uint16_t* qkva, const uint16_t* w_kv_norm, const uint16_t* W_uk, const uint16_t* cos_row,
+                 const uint16_t* sin_row, int nh, int d_n, int d_r, int d_c, float eps, uint16_t* c_row,
+                 uint16_t* k_pe_row, uint16_t* ql_nope, uint16_t* q_pe) {
+  int q_out = nh * (d_n + d_r);
+  or_rmsnorm(qkva + q_out, w_kv_norm, d_c, eps, c_row);
+  or_rope(qkva + q_out + d_c, cos_row, sin_row, d_r, k_pe_row);
+  float qn[512];
+  for (int h = 0; h < nh; ++h) {
+    const uint16_t* q = qkva + h * (d_n + d_r);
+    or_rope(q + d_n, cos_row, sin_row, d_r, q_pe + h * d_r);
+    for (int n = 0; n < d_n; ++n) qn[n] = b2f(q[n]);
+    const uint16_t* Wh = W_uk + (size_t)h * d_n * d_c;
+    for (int c = 0; c < d_c; ++c) ql_nope[h * d_c + c] = f2b(dot_lanes_col(qn, Wh + c, d_n, d_c));
+  }
+}
+
+/* ------------------------------------------------------------------------------------------ */
+/* MLA attend (numpy_ref.py:110-149), VALU spec                                                */
+
+/* Score of one (head, position): the 512 latent columns are summed as 4 sequential fma chains of
+ * d_c/4 columns each (chain k covers [k d_c/4, (k+1) d_c/4)), the 64 rope columns as a fifth
+ * sequential chain, then s = ((((n0 + n1) + n2) + n3) + pe) * scale. */
+static inline float attn_score(const float* ql, const float* qp, const uint16_t* ck, const uint16_t* kp, int d_c,
+                               int d_r, float scale) {
+  int len = d_c / 4;
+  float n[4];
+  for (int k = 0; k < 4; ++k) {
+    float a = 0.0f;
+    for (int c = k * len; c < (k + 1) * len; ++c) a = fmaf(ql[c], b2f(ck[c]), a);
+    n[k] = a;
+  }
+  float b = 0.0f;
+  for (int r = 0; r < d_r; ++r) b = fmaf(qp[r], b2f(kp[r]), b);
+  float s = n[0] + n[1];
+  s = s + n[2];
+  s = s + n[3];
+  s = s + b;
+  return s * scale;
+}
+
+/* partials [n_splits][nh][prow] f32: o at [0, d_c), lse at d_c. Splits of `split` positions over
+ * rows [0, step]; each split is processed in tiles of 32 positions with the online softmax:
+ *   m_new = max(m, max s); alpha = exp(m - m_new); p = exp(s - m_new);
+ *   l = l*alpha + sum_t p (sequential t); acc = acc*alpha + sum_t bf16(p)*v (sequential t, fma)
+ *   o = acc / l; lse = m + log(l). Empty split: o = 0, lse = -inf.
+ * scores (optional) [nh][s_scores] f32 gets the scaled scores. */
+void or_mla_attend(const uint16_t* ql_nope, const uint16_t* q_pe, const uint16_t* c_kv, const uint16_t* k_pe,
+                   int step, float scale, int split, int n_splits, int nh, int d_c, int d_r, int prow, float* partials,
+                   float* scores, int s_scores) {
+  float* qlf = (float*)malloc(sizeof(float) * nh * d_c);
+  float* qpf = (float*)malloc(sizeof(float) * nh * d_r);
+  for (int i = 0; i < nh * d_c; ++i) qlf[i] = b2f(ql_nope[i]);
+  for (int i = 0; i < nh * d_r; ++i) qpf[i] = b2f(q_pe[i]);
+#pragma omp parallel for schedule(dynamic) collapse(2)
+  for (int j = 0; j < n_splits; ++j) {
+    for (int h = 0; h < nh; ++h) {
+      float* out = partials + ((size_t)j * nh + h) * prow;
+      int lo = j * split, hi = lo + split;
+      if (hi > step + 1) hi = step + 1;
+      if (lo > step) {
+        for (int c = 0; c < d_c; ++c) out[c] = 0.0f;
+        out[d_c] = -INFINITY;
+        continue;
+      }
+      float m = -INFINITY, l = 0.0f;
+      float acc[1024];
+      float tile_pv[1024];
+      for (int c = 0; c < d_c; ++c) acc[c] = 0.0f;
+      float s[ATTN_TILE];
+      for (int t0 = lo; t0 < hi; t0 += ATTN_TILE) {
+        int t1 = t0 + ATTN_TILE < hi ? t0 + ATTN_TILE : hi;
+        int nt = t1 - t0;
+        float mt = -INFINITY;
+        for (int t = 0; t < nt; ++t) {
+          s[t] = attn_score(qlf + h * d_c, qpf + h * d_r, c_kv + (size_t)(t0 + t) * d_c, k_pe + (size_t)(t0 + t) * d_r,
+                            d_c, d_r, scale);
+          if (scores && t0 + t < s_scores) scores[(size_t)h * s_scores + t0 + t] = s[t];
+          if (s[t] > mt) mt = s[t];
+        }
+        float m_new = m > mt ? m : mt;
+        float alpha = or_exp(m - m_new);
+        float psum = 0.0f;
+        float pb[ATTN_TILE];
+        for (int t = 0; t < nt; ++t) {
+          float p = or_exp(s[t] - m_new);
+          psum = psum + p;
+          pb[t] = bf16r(p);
+        }
+        l = l * alpha + psum;
+        for (int c = 0; c < d_c; ++c) tile_pv[c] = 0.0f;
+        for (int t = 0; t < nt; ++t) {
+          const uint16_t* v = c_kv + (size_t)(t0 + t) * d_c;
+          for (int c = 0; c < d_c; ++c) tile_pv[c] = fmaf(pb[t], b2f(v[c]), tile_pv[c]);
+        }
+        for (int c = 0; c < d_c; ++c) acc[c] = acc[c] * alpha + tile_pv[c];
+        m = m_new;
+      }
+      for (int c = 0; c < d_c; ++c) out[c] = acc[c] / l;
+      out[d_c] = m + or_log(l);
+    }
+  }
+  free(qlf);
+  free(qpf);
+}
+
+/* numpy_ref.py:152-174: merge the live splits of each head, o rounded to bf16, then
+ * attn[h*d_v + v] = bf16(dot_lanes(o[h], W_uv[h][v])). Also returns o_bf [nh][d_c] if non-NULL.
+ * Merge order: M = max lse; w_j = exp(lse_j - M); num = sum_j w_j o_j (sequential, fma);
+ * den = sum_j w_j (sequential); o = num / den. */
+void or_mla_merge_uv(const float* partials, const uint16_t* W_uv, int step, int split, int nh, int d_c, int d_v,
+                     int prow, uint16_t* attn, uint16_t* o_bf_out) {
+  int live = (step + 1 + split - 1) / split;
+  float* obf = (float*)malloc(sizeof(float) * nh * d_c);
+  float* w = (float*)malloc(sizeof(float) * live);
+  for (int h = 0; h < nh; ++h) {
+    float M = -INFINITY;
+    for (int j = 0; j < live; ++j) {
+      float v = partials[((size_t)j * nh + h) * prow + d_c];
+      if (v > M) M = v;
+    }
+    float den = 0.0f;
+    for (int j = 0; j < live; ++j) {
+      w[j] = or_exp(partials[((size_t)j * nh + h) * prow + d_c] - M);
+      den = den + w[j];
+    }
+    for (int c = 0; c < d_c; ++c) {
+      float num = 0.0f;
+      for (int j = 0; j < live; ++j) num = fmaf(w[j], partials[((size_t)j * nh + h) * prow + c], num);
+      obf[h * d_c + c] = bf16r(num / den);
+      if (o_bf_out) o_bf_out[h * d_c + c] = f2b(obf[h * d_c + c]);
+    }
+  }
+#pragma omp parallel for schedule(static)
+  for (int r = 0; r < nh * d_v; ++r) {
+    int h = r / d_v;
+    attn[r] = f2b(dot_lanes_bf(W_uv + (size_t)r * d_c, obf + h * d_c, d_c));
+  }
+  free(obf);
+  free(w);
+}
+
+/* ------------------------------------------------------------------------------------------ */
+/* MoE (numpy_ref.py:205-292, 316-321)                                                         */
+
+/* softmax of the spec: m = max; e_i = exp(l_i - m); sum by the xor butterfly over the
+ * smallest power of two >= n lanes (lane i holds e_i, zeros past n); p_i = e_i / sum. */
+static void softmax_spec(const float* logits, int n, float* p) {
+  float m = -INFINITY;
+  for (int i = 0; i < n; ++i) if (logits[i] > m) m = logits[i];
+  int nl = 1;
+  while (nl < n) nl <<= 1;
+  float acc[256];
+  for (int i = 0; i < nl; ++i) acc[i] = 0.0f;
+  for (int i = 0; i < n; ++i) { p[i] = or_exp(logits[i] - m); acc[i] = p[i]; }
+  for (int off = 1; off < nl; off <<= 1) {
+    float tmp[256];
+    for (int l = 0; l < nl; ++l) tmp[l] = acc[l] + acc[l ^ off];
+    memcpy(acc, tmp, sizeof(float) * nl);
+  }
+  float sum = acc[0];
+  for (int i = 0; i < n; ++i) p[i] = p[i] / sum;
+}
+
+/* moe_router_norm (numpy_ref.py:237-245): h = rmsnorm(x_res) when norm_w, logits = W_gate h (f32),
+ * softmax, top-k by repeated argmax (lowest index on ties), forced experts appended at 1.0. */
+void or_moe_router(const uint16_t* x, const uint16_t* norm_w, float eps, const uint16_t* W_gate, int E, int H,
+                   int topk, int n_forced, float scaling, uint16_t* h_out, float* logits, float* topk_w,
+                   int32_t* routing, int32_t* mask) {
+  uint16_t* h = (uint16_t*)malloc(sizeof(uint16_t) * H);
+  if (norm_w) or_rmsnorm(x, norm_w, H, eps, h);
+  else memcpy(h, x, sizeof(uint16_t) * H);
+  if (h_out) memcpy(h_out, h, sizeof(uint16_t) * H);
+  or_linear_f32(W_gate, h, E, H, logits);
+  float p[256], rem[256];
+  softmax_spec(logits, E, p);
+  memcpy(rem, p, sizeof(float) * E);
+  int ids[64];
+  for (int k = 0; k < topk; ++k) {
+    int best = 0;
+    for (int e = 1; e < E; ++e) if (rem[e] > rem[best]) best = e;
+    ids[k] = best;
+    rem[best] = -INFINITY;
+    topk_w[k] = p[best] * scaling;
+  }
+  for (int f = 0; f < n_forced; ++f) { ids[topk + f] = E + f; topk_w[topk + f] = 1.0f; }
+  int n_slots = topk + n_forced, n_total = E + n_forced;
+  for (int e = 0; e < n_total; ++e) routing[e] = 0;
+  for (int k = 0; k < n_slots; ++k) routing[ids[k]] = k + 1;
+  for (int e = 0; e <= n_total; ++e) mask[e] = -1;
+  for (int k = 0; k < n_slots; ++k) mask[k] = ids[k];
+  mask[n_total] = n_slots;
+  free(h);
+}
+
+/* gate|up GEMV with SiLU in the epilogue (numpy_ref.py:256-292 fused): for slot s < count,
+ * expert e = mask[s]: g = bf16(dot(W13[e][i], h)), u = bf16(dot(W13[e][I+i], h)),
+ * act[s][i] = bf16(silu(g) * u). */
+void or_moe_w13_silu(const uint16_t* h, const uint16_t* W13, const int32_t* mask, int n_slots, int I, int H,
+                     uint16_t* act) {
+  float* hf = (float*)malloc(sizeof(float) * H);
+  for (int i = 0; i < H; ++i) hf[i] = b2f(h[i]);
+  int n_total_plus = 0;
+  (void)n_total_plus;
+  for (int s = 0; s < n_slots; ++s) {
+    int e = mask[s];
+    const uint16_t* W = W13 + (size_t)e * 2 * I * H;
+#pragma omp parallel for schedule(static)
+    for (int i = 0; i < I; ++i) {
+      float g = bf16r(dot_lanes_bf(W + (size_t)i * H, hf, H));
+      float u = bf16r(dot_lanes_bf(W + (size_t)(I + i) * H, hf, H));
+      act[(size_t)s * I + i] = f2b(or_silu(g) * u);
+    }
+  }
+  free(hf);
+}
+
+/* out8[s][n] = bf16(dot(W2[e][n], act[s])), K = I. */
+void or_moe_w2(const uint16_t* act, const uint16_t* W2, const int32_t* mask, int n_slots, int I, int H,
+               uint16_t* out8) {
+  float* af = (float*)malloc(sizeof(float) * I);
+  for (int s = 0; s < n_slots; ++s) {
+    int e = mask[s];
+    for (int i = 0; i < I; ++i) af[i] = b2f(act[(size_t)s * I + i]);
+    const uint16_t* W = W2 + (size_t)e * H * I;
+#pragma omp parallel for schedule(static)
+    for (int n = 0; n < H; ++n) out8[(size_t)s * H + n] = f2b(dot_lanes_bf(W + (size_t)n * I, af, I));
+  }
+  free(af);
+}
+
+/* numpy_ref.py:316-321: acc = x; acc = acc + out8[k] * w[k] (mul then add) for k in slot order. */
+void or_moe_combine(const uint16_t* out8, const float* topk_w, const uint16_t* x_res, int n_slots, int H,
+                    uint16_t* out) {
+  for (int n = 0; n < H; ++n) {
+    float acc = b2f(x_res[n]);
+    for (int k = 0; k < n_slots; ++k) {
+      float t = b2f(out8[(size_t)k * H + n]) * topk_w[k];
+      acc = acc + t;
+    }
+    out[n] = f2b(acc);
+  }
+}
+
+/* Layer-0 dense MLP: h = rmsnorm(x_res, w_norm2); act_i = bf16(silu(bf16(Wg_i h)) * bf16(Wu_i h));
+ * x_res = bf16(dot(Wd[n], act) + x_res[n]). W_gu [2I][H] (gate rows then up rows), W_d [H][I]. */
+void or_dense_mlp(const uint16_t* x_res, const uint16_t* w_norm2, float eps, const uint16_t* W_gu,
+                  const uint16_t* W_d, int I, int H, uint16_t* h_out, uint16_t* act_out, uint16_t* x_out) {
+  uint16_t* h = (uint16_t*)malloc(sizeof(uint16_t) * H);
+  or_rmsnorm(x_res, w_norm2, H, eps, h);
+  if (h_out) memcpy(h_out, h, sizeof(uint16_t) * H);
+  int32_t mask[2] = {0, 1};
+  uint16_t* act = (uint16_t*)malloc(sizeof(uint16_t) * I);
+  or_moe_w13_silu(h, W_gu, mask, 1, I, H, act);
+  if (act_out) memcpy(act_out, act, sizeof(uint16_t) * I);
+  or_linear(W_d, act, NULL, 0.0f, x_res, H, I, x_out, NULL);
+  free(h);
+  free(act);
+}
+
+/* Greedy id: the lowest index among the maximal bf16 logits. */
+int64_t or_argmax_bf16(const uint16_t* logits, int64_t V) {
+  int64_t best = 0;
+  float bv = b2f(logits[0]);
+  for (int64_t i = 1; i < V; ++i) {
+    float v = b2f(logits[i]);
+    if (v > bv) { bv = v; best = i; }
+  }
+  return best;
+}
+
+/* ------------------------------------------------------------------------------------------ */
+/* Seeded generator: Philox4x32-10 (Salmon et al., SC'11) + Box-Muller with the spec's log and  */
+/* a polynomial sin/cos on a quadrant-reduced angle.                                           */
+
+static inline void philox_round(uint32_t* c, const uint32_t* k) {
+  const uint64_t M0 = 0xD2511F53ull, M1 = 0xCD9E8D57ull;
+  uint64_t p0 = M0 * c[0], p1 = M1 * c[2];
+  uint32_t hi0 = (uint32_t)(p0 >> 32), lo0 = (uint32_t)p0;
+  uint32_t hi1 = (uint32_t)(p1 >> 32), lo1 = (uint32_t)p1;
+  uint32_t n0 = hi1 ^ c[1] ^ k[0];
+  uint32_t n1 = lo1;
+  uint32_t n2 = hi0 ^ c[3] ^ k[1];
+  uint32_t n3 = lo0;
+  c[0] = n0; c[1] = n1; c[2] = n2; c[3] = n3;
+}
+
+/* Raw Philox4x32-10 of a full counter and key (for the published known-answer vectors). */
+void or_philox4x32_raw(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4]) {
+  uint32_t c[4] = {ctr[0], ctr[1], ctr[2], ctr[3]};
+  uint32_t k[2] = {key[0], key[1]};
+  for (int r = 0; r < 10; ++r) {
+    philox_round(c, k);
+    if (r < 9) { k[0] += 0x9E3779B9u; k[1] += 0xBB67AE85u; }
+  }
+  memcpy(out, c, 16);
+}
+
+void or_philox4x32(uint64_t seed, uint64_t block, uint32_t stream, uint32_t out[4]) {
+  uint32_t c[4] = {(uint32_t)block, (uint32_t)(block >> 32), stream, 0x5EEDu};
+  uint32_t k[2] = {(uint32_t)seed, (uint32_t)(seed >> 32)};
+  for (int r = 0; r < 10; ++r) {
+    philox_round(c, k);
+    if (r < 9) { k[0] += 0x9E3779B9u; k[1] += 0xBB67AE85u; }
+  }
+  memcpy(out, c, 16);
+}
+
+static inline void sincos_quarter(float f, float* s, float* c) {
+  /* f in [0, 1): angle = f * pi/2 */
+  const float HALF_PI = 1.57079637f;
+  float t = f * HALF_PI;
+  float z = t * t;
+  float ps = -2.5052108e-8f;        /* -1/11! */
+  ps = ps * z + 2.7557319e-6f;      /* 1/9! */
+  ps = ps * z + -1.9841270e-4f;     /* -1/7! */
+  ps = ps * z + 8.3333333e-3f;      /* 1/5! */
+  ps = ps * z + -1.6666667e-1f;     /* -1/3! */
+  ps = ps * z + 1.0f;
+  *s = ps * t;
+  float pc = 2.0876757e-9f;         /* 1/12! */
+  pc = pc * z + -2.7557319e-7f;     /* -1/10! */
+  pc = pc * z + 2.4801587e-5f;      /* 1/8! */
+  pc = pc * z + -1.3888889e-3f;     /* -1/6! */
+  pc = pc * z + 4.1666668e-2f;      /* 1/4! */
+  pc = pc * z + -0.5f;
+  pc = pc * z + 1.0f;
+  *c = pc;
+}
+
+static inline void box_muller(uint32_t a, uint32_t b, float* z0, float* z1) {
+  const float INV24 = 5.96046448e-08f; /* 2^-24 */
+  float u1 = (float)((a >> 8) + 1u) * INV24;
+  float u2 = (float)(b >> 8) * INV24;
+  float r = sqrtf(-2.0f * or_log(u1));
+  float v = u2 * 4.0f;
+  int q = (int)v;
+  float f = v - (float)q;
+  float s, c;
+  sincos_quarter(f, &s, &c);
+  float cs, sn;
+  switch (q) {
+    case 0: cs = c; sn = s; break;
+    case 1: cs = -s; sn = c; break;
+    case 2: cs = -c; sn = -s; break;
+    default: cs = s; sn = -c; break;
+  }
+  *z0 = r * cs;
+  *z1 = r * sn;
+}
+
+/* Element i of stream `stream`: block i/4 of Philox, normals from (x0,x1) and (x2,x3). */
+float or_normal(uint64_t seed, uint32_t stream, uint64_t i) {
+  uint32_t x[4];
+  or_philox4x32(seed, i >> 2, stream, x);
+  float z[4];
+  box_muller(x[0], x[1], &z[0], &z[1]);
+  box_muller(x[2], x[3], &z[2], &z[3]);
+  return z[i & 3];
+}
+
+/* out[j] = bf16(normal(seed, stream, offset + j) * scale) for j < n. */
+void or_gen_normal_bf16(uint64_t seed, uint32_t stream, uint64_t offset, int64_t n, float scale, uint16_t* out) {
+#pragma omp parallel for schedule(static)
+  for (int64_t b = 0; b < (n + 3) / 4 + 1; ++b) {
+    uint64_t base = (offset & ~3ull) + (uint64_t)b * 4;
+    uint32_t x[4];
+    or_philox4x32(seed, base >> 2, stream, x);
+    float z[4];
+    box_muller(x[0], x[1], &z[0], &z[1]);
+    box_muller(x[2], x[3], &z[2], &z[3]);
+    for (int k = 0; k < 4; ++k) {
+      uint64_t i = base + k;
+      if (i < offset || i >= offset + (uint64_t)n) continue;
+      out[i - offset] = f2b(z[k] * scale);
+    }
+  }
+}
+
+/* Uniform ids in [0, V): (u32 * V) >> 32 of Philox block i/4, word i%4. */
+void or_gen_tokens(uint64_t seed, uint32_t stream, int64_t n, int64_t V, int64_t* out) {
+  for (int64_t i = 0; i < n; ++i) {
+    uint32_t x[4];
+    or_philox4x32(seed, (uint64_t)i >> 2, stream, x);
+    out[i] = (int64_t)(((uint64_t)x[i & 3] * (uint64_t)V) >> 32);
+  }
+}
+
+/* Element-wise array forms of the spec's exp, log and silu (for tests). */
+void or_exp_array(const float* x, float* y, int64_t n) { for (int64_t i = 0; i < n; ++i) y[i] = or_exp(x[i]); }
+void or_log_array(const float* x, float* y, int64_t n) { for (int64_t i = 0; i < n; ++i) y[i] = or_log(x[i]); }
+void or_silu_array(const float* x, float* y, int64_t n) { for (int64_t i = 0; i < n; ++i) y[i] = or_silu(x[i]); }
+
+int or_num_threads(void) {
+#ifdef _OPENMP
+  return omp_get_max_threads();
+#else
+  return 1;
+#endif
+}
+
+void or_set_num_threads(int n) {
+#ifdef _OPENMP
+  omp_set_num_threads(n);
+#else
+  (void)n;
+#endif
+}

@@ -1,0 +1,146 @@
+"""Whole-model composition of the oracle: one batch-1 decode step of DeepSeek-V2-Lite.
+
+TEST INFRASTRUCTURE ONLY (see oracle/oracle.py). It chains the per-kernel oracle functions in the
+order of the reference's task graph (fleet/graph_plan.py:380-603, the --final stack of
+harness/run_fleet.py:291-298): embed, then per layer norm1+qkva, mla_prep (with the cache
+append), mla_attend, merge+W_uv, o_proj with the residual, then the dense MLP (layer 0) or the
+router, w13+silu, w2 and the combine (layers >= 1), then the final norm, the LM head and the
+argmax. numpy_ref.py has no whole-model driver (numpy_ref.py:1-26); this composition follows HF
+modeling_deepseek.py:1193-1234 (decoder layer: residual around attention and around the MLP).
+
+Weights are a mapping of the plan's packed keys (pack_weights names, suffix _l per layer) to
+uint16 arrays; a mapping may also provide .expert(key, e) to hand over one expert slab lazily.
+"""
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import oracle as O
+
+
+@dataclass(frozen=True)
+class Cfg:
+    H: int = 2048
+    NH: int = 16
+    D_N: int = 128
+    D_R: int = 64
+    D_V: int = 128
+    D_C: int = 512
+    V: int = 102400
+    L: int = 27
+    I_DENSE: int = 10944
+    I_MOE: int = 1408
+    E: int = 64
+    TOPK: int = 6
+    N_SHARED: int = 2
+    eps: float = 1e-6
+    scale: float = float(np.float32(1.0 / np.sqrt(192.0)))
+    split: int = 32
+    n_splits: int = 33
+
+    @property
+    def Q_OUT(self):
+        return self.NH * (self.D_N + self.D_R)
+
+
+def _expert(W, key, e):
+    if hasattr(W, "expert"):
+        return W.expert(key, e)
+    return W[key][e]
+
+
+class Cache:
+    """Latent cache of every layer: c_kv [L][S_max, D_C], k_pe [L][S_max, D_R] (bf16 bits)."""
+
+    def __init__(self, cfg, s_max, layers=None):
+        n = cfg.L if layers is None else layers
+        self.c_kv = [np.zeros((s_max, cfg.D_C), np.uint16) for _ in range(n)]
+        self.k_pe = [np.zeros((s_max, cfg.D_R), np.uint16) for _ in range(n)]
+        self.s_max = s_max
+
+
+def layer_step(cfg, W, cache, cos, sin, x_res, step, l, rec=None):
+    """One decoder layer at position `step`; returns the new x_res. rec (a dict) collects the
+    boundaries under the harness's keys (harness/common.py:44-59)."""
+    c = cfg
+    qkva, h1 = O.linear(W[f"W_qkva_{l}"], x_res, norm_w=W[f"w_norm1_{l}"], eps=c.eps)
+    c_row, k_pe_row, ql, qp = O.mla_prep(qkva, W[f"w_kv_norm_{l}"], W[f"W_uk_{l}"], cos[step], sin[step],
+                                        c.NH, c.D_N, c.D_R, c.D_C, c.eps)
+    cache.c_kv[l][step] = c_row
+    cache.k_pe[l][step] = k_pe_row
+    partials = O.mla_attend(ql, qp, cache.c_kv[l], cache.k_pe[l], step, c.scale, c.split, c.n_splits)
+    attn, obf = O.mla_merge_uv(partials, W[f"W_uv_{l}"], step, c.split)
+    x_attn, _ = O.linear(W[f"W_o_{l}"], attn, res=x_res)
+    if rec is not None:
+        rec.update({f"L{l}.B1.norm1": h1, f"L{l}.B2.q": qkva[:c.Q_OUT], f"L{l}.kva": qkva[c.Q_OUT:],
+                    f"L{l}.B3.c_kv": c_row, f"L{l}.B3.k_pe": k_pe_row, f"L{l}.B4.q_pe": qp,
+                    f"L{l}.ql_nope": ql, f"L{l}.partials": partials, f"L{l}.o_merged": obf,
+                    f"L{l}.B6.attn": attn, f"L{l}.B7.x_res_attn": x_attn})
+    if l == 0:
+        h, act, x_out = O.dense_mlp(x_attn, W[f"w_norm2_{l}"], W[f"W_gu_{l}"], W[f"W_down_{l}"], c.eps)
+        if rec is not None:
+            rec.update({f"L{l}.norm2": h, f"L{l}.act": act, f"L{l}.B13.layer_out": x_out})
+        return x_out, None
+    h, logits, topk_w, routing, mask = O.moe_router(x_attn, W[f"W_gate_{l}"], norm_w=W[f"w_norm2_{l}"], eps=c.eps,
+                                                    topk=c.TOPK, n_forced=c.N_SHARED)
+    n_slots = c.TOPK + c.N_SHARED
+    ids = [int(e) for e in mask[:n_slots]]
+    W13 = np.stack([_expert(W, f"W13_{l}", e) for e in ids])
+    W2 = np.stack([_expert(W, f"W2_{l}", e) for e in ids])
+    local = np.arange(n_slots + 1, dtype=np.int32)
+    local[n_slots] = n_slots
+    act = O.moe_w13_silu(h, W13, local, n_slots)
+    out8 = O.moe_w2(act, W2, local, n_slots)
+    x_out = O.moe_combine(out8, topk_w, x_attn)
+    if rec is not None:
+        rec.update({f"L{l}.norm2": h, f"L{l}.B8.router_logits": logits, f"L{l}.B9.topk_idx": mask[:c.TOPK].copy(),
+                    f"L{l}.B10.topk_w": topk_w, f"L{l}.routing": routing, f"L{l}.mask": mask,
+                    f"L{l}.act8": act, f"L{l}.out8": out8, f"L{l}.B13.layer_out": x_out})
+    return x_out, ids
+
+
+def decode_step(cfg, W, cache, cos, sin, token, step, layers=None, head=True, rec=None):
+    """Embed `token` at position `step`, run the layers and (head) the LM head + argmax.
+    Returns (next_token or None, route ids per MoE layer [list of 8 ids], final x_res)."""
+    n = cfg.L if layers is None else layers
+    x = np.ascontiguousarray(W["W_embed"][int(token)])
+    routes = []
+    for l in range(n):
+        x, ids = layer_step(cfg, W, cache, cos, sin, x, step, l, rec)
+        if ids is not None:
+            routes.append(ids)
+    if not head:
+        return None, routes, x
+    logits, hf = O.linear(W["W_lm"], x, norm_w=W["w_final_norm"], eps=cfg.eps)
+    tok = O.argmax_bf16(logits)
+    if rec is not None:
+        rec.update({"head.B14.norm": hf, "head.B15.logits": logits, "head.B16.token": np.array([tok], np.int64)})
+    return tok, routes, x
+
+
+def generate(cfg, W, cache, cos, sin, prompt, n_new, layers=None, prefill_from=0, on_token=None):
+    """Prefill positions [prefill_from, len(prompt)-1) without the head (the cache rows before
+    prefill_from must already be in `cache`), then n_new greedy steps from position len(prompt)-1.
+    Returns (ids [n_new], routes [n_new][moe layers][8])."""
+    n_prompt = len(prompt)
+    for pos in range(prefill_from, n_prompt - 1):
+        decode_step(cfg, W, cache, cos, sin, prompt[pos], pos, layers, head=False)
+    ids, routes = [], []
+    tok = int(prompt[-1])
+    for i in range(n_new):
+        step = n_prompt - 1 + i
+        tok, r, _ = decode_step(cfg, W, cache, cos, sin, tok, step, layers, head=True)
+        ids.append(tok)
+        routes.append(r)
+        if on_token is not None:
+            on_token(i, tok, r)
+    return ids, routes
+
+
+def rope_tables(s_max, d_r=64, theta=10000.0):
+    """cos / sin [s_max, d_r] as bf16 bits: HF layout cat(freqs, freqs), plain RoPE, computed in
+    float64 and rounded to float32 then bf16 (fleet/tasks/kernel_tests.py:325-330)."""
+    inv_freq = 1.0 / (theta ** (np.arange(0, d_r, 2, dtype=np.float64) / d_r))
+    freqs = np.arange(s_max, dtype=np.float64)[:, None] * inv_freq[None, :]
+    emb = np.concatenate([freqs, freqs], axis=-1)
+    return O.f32_to_bf16(np.cos(emb).astype(np.float32)), O.f32_to_bf16(np.sin(emb).astype(np.float32))
