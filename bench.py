@@ -1,0 +1,182 @@
+#!/usr/bin/env python3
+"""Benchmark of BASELINE.json's metric: us per decoded token (batch 1, ctx 1024) and the fraction of
+the HBM roofline, on one MI355X.
+
+Workload: the full 27-layer DeepSeek-V2-Lite with random-init bf16 weights
+~N(0, 0.02) from a seed (norm weights 1.0), a 1,024-token prompt drawn uniformly from the 102,400-id
+vocabulary with a seed, an untimed prefill that writes the latent caches of positions 0..1022
+through the same persistent kernel (teacher-forced iterations, head skipped), then greedy decode
+at batch 1. A "step" is one decoded token; `--steps` tokens are timed, starting at position 1023
+(so every timed token attends over 1,024..1,024+steps-1 positions), after `--warmup` untimed
+tokens at the same positions. Inputs are resident in HBM when the timed region starts.
+
+value        us per decoded token: HIP-event time of the timed fx_run launch / steps
+roofline     algorithmic HBM bytes per token (every weight the token touches once -- 8 of the 66
+             experts per MoE layer -- plus the latent-cache rows read and the embedding row; mean
+             over the timed tokens) / us per token, against the published 8 TB/s
+cpu_baseline the CPU oracle (oracle/, a C port of harness/numpy_ref.py semantics, OpenMP) decoding
+             the first `--cpu-tokens` tokens of the same run on this host's cores, checked for
+             equal ids; weights it touches are copied to host memory before its timed region
+
+    python bench.py [--gpus 1] [--steps 32] [--warmup 2]
+"""
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "fleet-amd-task_amd"))
+
+import numpy as np  # noqa: E402
+
+from fleet import build_graph as B  # noqa: E402
+from fleet import graph_plan as G  # noqa: E402
+from fleet import pack_weights as P  # noqa: E402
+from fleet import runtime as R  # noqa: E402
+
+HBM_PEAK_GBPS = 8000.0
+METRIC = "µs/decoded token (batch 1, ctx 1024) and % of HBM roofline on 1 MI355X"
+
+
+def log(*a):
+    print("[bench]", *a, file=sys.stderr, flush=True)
+
+
+def cpu_baseline(rt, runner, bufs, plan, prompt, ctx, n_tok, gpu_ids):
+    """Time the oracle on the host decoding n_tok tokens from position ctx - 1 with the GPU prefill's
+    cache rows 0..ctx-2 (test infrastructure: the checker, run here only as the reported baseline)."""
+    sys.path.insert(0, str(ROOT))
+    from oracle import oracle as O
+    from oracle import model as M
+
+    d = plan.dims
+    cfg = M.Cfg(H=d.H, NH=d.NH, D_N=d.D_N, D_R=d.D_R, D_V=d.D_V, D_C=d.D_C, V=d.V, L=d.L, I_DENSE=d.I_DENSE,
+                I_MOE=d.I_MOE, E=d.E, TOPK=d.TOPK, N_SHARED=d.N_SHARED, eps=plan.eps, scale=plan.scale,
+                split=plan.split, n_splits=plan.n_splits)
+    cache = M.Cache(cfg, plan.s_max)
+    for l in range(d.L):
+        cache.c_kv[l][:ctx - 1] = runner.host[f"c_kv_{l}"].download()[:ctx - 1]
+        cache.k_pe[l][:ctx - 1] = runner.host[f"k_pe_{l}"].download()[:ctx - 1]
+    cos, sin = M.rope_tables(plan.s_max)
+    # host copies of every weight the sampled tokens touch (routes from the GPU run's route log)
+    W = {}
+    for key in ("W_embed", "W_lm", "w_final_norm"):
+        W[key] = bufs[key].download()
+    for l in range(d.L):
+        for key in (f"w_norm1_{l}", f"w_norm2_{l}", f"W_qkva_{l}", f"w_kv_norm_{l}", f"W_uk_{l}", f"W_uv_{l}", f"W_o_{l}"):
+            W[key] = bufs[key].download()
+    W["W_gu_0"], W["W_down_0"] = bufs["W_gu_0"].download(), bufs["W_down_0"].download()
+    rl = runner.host["route_log"].download()
+    experts = {}
+    for l in range(1, d.L):
+        W[f"W_gate_{l}"] = bufs[f"W_gate_{l}"].download()
+        for i in range(n_tok):
+            for e in rl[i, l - 1].tolist():
+                for key, per in ((f"W13_{l}", 2 * d.I_MOE * d.H), (f"W2_{l}", d.H * d.I_MOE)):
+                    if (key, e) not in experts:
+                        shape = bufs[key].shape[1:]
+                        experts[(key, e)] = bufs[key].download_range(e * per, per).reshape(shape)
+
+    class HostW(dict):
+        def expert(self, key, e):
+            return experts[(key, e)]
+
+    Wh = HostW(W)
+    threads = O.num_threads()
+    tok = int(prompt[ctx - 1])
+    times, ids = [], []
+    for i in range(n_tok):
+        t0 = time.perf_counter()
+        tok, _, _ = M.decode_step(cfg, Wh, cache, cos, sin, tok, ctx - 1 + i, d.L, True)
+        times.append(time.perf_counter() - t0)
+        ids.append(tok)
+    return {"value": round(1e6 * statistics.median(times), 1), "unit": "µs/token", "cores": threads,
+            "kind": "port", "sample": f"{n_tok} greedy decode tokens (positions {ctx - 1}..{ctx - 2 + n_tok}) of the "
+                                      f"same 27-layer model and prompt; oracle/fleet_oracle.c with {threads} OpenMP "
+                                      f"threads, weights resident in host memory; median per token",
+            "ids_equal_gpu": ids == gpu_ids[:n_tok]}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=32, help="timed decode tokens")
+    ap.add_argument("--warmup", type=int, default=2, help="untimed decode tokens before the timed ones")
+    ap.add_argument("--ctx", type=int, default=1024, help="prompt length (positions attended by the first token)")
+    ap.add_argument("--seed", type=int, default=20261201)
+    ap.add_argument("--cpu-tokens", type=int, default=2)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--n-splits", type=int, default=None, help="attention splits (default: 32-position splits)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (this build has no multi-GPU path; --gpus {args.gpus} is not "
+              f"supported): run it with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    if int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py is single-process, single-GPU", file=sys.stderr)
+        sys.exit(2)
+
+    d = P.REAL_DIMS
+    ctx, K, Wm = args.ctx, args.steps, args.warmup
+    s_max = ctx + max(K, Wm, 1)
+    rt = R.Runtime(0)
+    log("device", rt.info())
+    t0 = time.time()
+    bufs = P.fill_seeded(rt, d, args.seed, d.L, True)
+    gen_s = time.time() - t0
+    log(f"seeded weights: {P.packed_bytes(d) / 2**30:.2f} GiB in {gen_s:.1f} s")
+    prompt = P.prompt_ids(args.seed, ctx, d.V)
+    plan = G.build_plan(d, s_max, d.L, True, n_splits=args.n_splits)
+    meta = B.make_meta(rt, s_max, prompt)
+    cap = B.make_capture(rt, plan)
+    runner = B.build(rt, bufs, cap, meta, d, s_max, d.L, True)
+    log(f"plan: {len(runner.stages)} stages/iteration, {plan.n_splits} splits of {plan.split}, s_max {s_max}")
+    t0 = time.time()
+    runner.run(ctx - 1, 0, ctx)
+    prefill_s = time.time() - t0
+    log(f"prefill of {ctx - 1} positions: {prefill_s:.2f} s ({1e6 * prefill_s / (ctx - 1):.0f} us/position, head skipped)")
+    if Wm > 0:
+        runner.run(Wm, ctx - 1, ctx)
+        log(f"warmup: {Wm} tokens, {1e3 * rt.last_run_ms() / Wm:.1f} us/token")
+    t0 = time.perf_counter()
+    runner.run(K, ctx - 1, ctx)
+    wall_ms = 1e3 * (time.perf_counter() - t0)
+    ev_ms = rt.last_run_ms()
+    iter_us = runner.timing_us()
+    us_tok = 1e3 * ev_ms / K
+    ids = runner.host["tokens"].download()[ctx:ctx + K].tolist()
+    mean_bytes = sum(P.bytes_per_token(d, ctx + i) for i in range(K)) / K
+    achieved = mean_bytes / (us_tok * 1e-6) / 1e9
+    log(f"decode: {us_tok:.1f} us/token (event), wall {wall_ms / K * 1e3:.1f} us/token, iteration median "
+        f"{statistics.median(iter_us):.1f} us; {achieved:.0f} GB/s = {100 * achieved / HBM_PEAK_GBPS:.1f}% of 8 TB/s")
+    log(f"ids {ids}")
+    out = {
+        "metric": METRIC, "value": round(us_tok, 2), "unit": "µs/token", "n_gpus": 1, "steps": K, "warmup": Wm,
+        "ms_per_step": round(us_tok / 1e3, 5), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic: seeded N(0,0.02) bf16 weights, seeded uniform 1024-token prompt",
+        "config": {"workload": "BASELINE configs[3]: DeepSeek-V2-Lite 27 layers, 1024-token prompt (prefill untimed), "
+                               "greedy decode at batch 1", "layers": d.L, "batch": 1, "ctx": ctx, "decode_tokens": K,
+                   "splits": plan.n_splits, "seed": args.seed},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "bytes_per_token": int(mean_bytes), "kernel": "fx_persistent"},
+        "iter_us_median": round(statistics.median(iter_us), 2), "prefill_s": round(prefill_s, 2),
+        "ids": ids,
+    }
+    if not args.no_cpu_baseline:
+        log(f"cpu baseline: oracle on {args.cpu_tokens} tokens")
+        try:
+            out["cpu_baseline"] = cpu_baseline(rt, runner, bufs, plan, prompt, ctx, args.cpu_tokens, ids)
+            log(f"cpu baseline {out['cpu_baseline']['value']} us/token on {out['cpu_baseline']['cores']} threads, "
+                f"ids equal: {out['cpu_baseline']['ids_equal_gpu']}")
+        except Exception as e:  # the baseline is reported, never the measured value
+            out["cpu_baseline"] = {"value": None, "error": repr(e)}
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -38,6 +38,8 @@ struct FxRunArgs {
   int64_t* tokens;
   uint32_t* sync;
   uint64_t* timing;
+  uint64_t* prof;      // [n_stages][256][2] stamps of iteration prof_iter, or null
+  int prof_iter;
   uint32_t epoch0;
 };
 
@@ -115,6 +117,7 @@ __global__ void __launch_bounds__(FX_THREADS) fx_persistent(FxRunArgs a) {
   env.tokens = a.tokens;
   env.sync = a.sync;
   env.lds = lds;
+  env.moe_e = -1;
   uint32_t epoch = a.epoch0;
   // the current stage descriptor is staged in LDS (read by every wave, never spilled to scratch)
   fx_stage* sst = (fx_stage*)(lds + LDS_STAGE);
@@ -127,11 +130,18 @@ __global__ void __launch_bounds__(FX_THREADS) fx_persistent(FxRunArgs a) {
     env.iter = it;
     env.step = a.step0 + it;
     if (env.worker == 0 && threadIdx.x == 0 && a.timing) a.timing[it] = __builtin_amdgcn_s_memrealtime();
+    const bool prof = a.prof && it == a.prof_iter;
     for (int s = 0; s < a.n_stages; ++s) {
       stage_in(a.stages + s);
       const int sync_kind = sst->sync;
       const bool skip = (sst->flags & FX_F_HEAD) && (env.step + 1 < env.n_prompt);
+      if (prof && threadIdx.x == 0) a.prof[((size_t)s * FX_BLOCKS + b) * 2] = __builtin_amdgcn_s_memrealtime();
       if (!skip) run_stage(*sst, env);
+      if (prof) {
+        wait_mem();
+        __syncthreads();
+        if (threadIdx.x == 0) a.prof[((size_t)s * FX_BLOCKS + b) * 2 + 1] = __builtin_amdgcn_s_memrealtime();
+      }
       if (sync_kind != FX_SYNC_NONE) worker_sync(a.sync, b, ++epoch);
     }
   }
@@ -163,6 +173,7 @@ __global__ void __launch_bounds__(FX_THREADS) fx_stage_kernel(fx_stage st, int s
   env.tokens = tokens;
   env.sync = sync;
   env.lds = lds;
+  env.moe_e = -1;
   env.iter = iter;
   env.step = step;
   run_stage(st, env);
@@ -293,6 +304,10 @@ struct fx_ctx {
   fx_stage* d_epi = nullptr;
   int n_epi = 0;
   std::vector<fx_stage> h_stages, h_epi;
+  hipEvent_t ev0 = nullptr, ev1 = nullptr;
+  uint64_t* prof = nullptr;
+  size_t prof_words = 0;
+  int prof_iter = -1;
 };
 
 static int fail(fx_ctx* c, int code, const std::string& msg) {
@@ -353,6 +368,9 @@ int fx_destroy(fx_ctx* c) {
   if (c->timing) (void)hipFree(c->timing);
   if (c->d_stages) (void)hipFree(c->d_stages);
   if (c->d_epi) (void)hipFree(c->d_epi);
+  if (c->ev0) (void)hipEventDestroy(c->ev0);
+  if (c->ev1) (void)hipEventDestroy(c->ev1);
+  if (c->prof) (void)hipFree(c->prof);
   delete c;
   return FX_OK;
 }
@@ -412,6 +430,8 @@ static int check_stage(fx_ctx* c, const fx_stage& s, int idx) {
         return bad("combine inputs");
       if ((s.flags & FX_F_NORM) && !s.w_norm) return bad("norm weight");
       if ((s.flags & FX_F_RESIDUAL) && !s.res) return bad("residual");
+      if ((s.flags & FX_F_RESIDUAL) && (s.n_rows + FX_WORKERS - 1) / FX_WORKERS > FX_MAX_RES_ROWS)
+        return bad("residual rows per worker exceed the LDS table");
       if ((s.flags & FX_F_WRITE_X) && !s.aux[2]) return bad("x_out");
       if ((s.flags & FX_F_ARGMAX) && !s.aux[3]) return bad("amax");
       break;
@@ -518,15 +538,56 @@ int fx_run(fx_ctx* c, int32_t iters, int32_t step0, int32_t n_prompt, int64_t* t
   a.tokens = tokens;
   a.sync = c->sync;
   a.timing = c->timing;
+  a.prof = nullptr;
+  a.prof_iter = -1;
+  if (c->prof_iter >= 0 && c->prof_iter < iters) {
+    const size_t words = (size_t)c->n_stages * FX_BLOCKS * 2;
+    if (c->prof_words < words) {
+      if (c->prof) HIPCHK(c, hipFree(c->prof));
+      HIPCHK(c, hipMalloc(&c->prof, words * 8));
+      c->prof_words = words;
+    }
+    HIPCHK(c, hipMemset(c->prof, 0, words * 8));
+    a.prof = c->prof;
+    a.prof_iter = c->prof_iter;
+  }
   a.epoch0 = c->epoch;
   void* args[] = {&a};
   hipStream_t s = (hipStream_t)stream;
+  if (!c->ev0) {
+    HIPCHK(c, hipEventCreate(&c->ev0));
+    HIPCHK(c, hipEventCreate(&c->ev1));
+  }
+  HIPCHK(c, hipEventRecord(c->ev0, s));
   HIPCHK(c, hipLaunchCooperativeKernel((const void*)fx_persistent, dim3(FX_BLOCKS), dim3(FX_THREADS), args, FX_LDS_BYTES, s));
+  HIPCHK(c, hipEventRecord(c->ev1, s));
   c->epoch += (uint32_t)total;
   c->last_iters = iters;
   HIPCHK(c, hipStreamSynchronize(s));
   HIPCHK(c, hipMemcpy(&err, c->sync + FX_FLAG_ERROR, 4, hipMemcpyDeviceToHost));
   if (err) return fail(c, FX_E_STATE, "a synchronisation wait timed out inside the persistent kernel");
+  return FX_OK;
+}
+
+int fx_set_profile(fx_ctx* c, int32_t iter) {
+  if (!c) return FX_E_ARG;
+  c->prof_iter = iter;
+  return FX_OK;
+}
+
+int fx_read_profile(fx_ctx* c, uint64_t* buf, int32_t n) {
+  if (!c || !buf) return -1;
+  if (!c->prof) return 0;
+  size_t m = (size_t)c->n_stages * FX_BLOCKS * 2;
+  if ((size_t)n < m) m = (size_t)n;
+  if (hipMemcpy(buf, c->prof, m * 8, hipMemcpyDeviceToHost) != hipSuccess) return -1;
+  return (int)m;
+}
+
+int fx_last_run_ms(fx_ctx* c, float* ms) {
+  if (!c || !ms) return FX_E_ARG;
+  if (!c->ev0) return fail(c, FX_E_STATE, "no run yet");
+  HIPCHK(c, hipEventElapsedTime(ms, c->ev0, c->ev1));
   return FX_OK;
 }
 

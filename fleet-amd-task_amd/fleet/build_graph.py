@@ -46,6 +46,7 @@ def compile_stages(plan, host):
     d = plan.dims
     cur, other = "x_res", "x_res_b"
     stages, epi = [], []
+    labels = []
     pend_embed = pend_combine = None
     sync_of = {G.GLOBAL: R.FX_SYNC_GLOBAL, G.XCD: R.FX_SYNC_XCD, G.NONE: R.FX_SYNC_NONE}
     B = lambda n: host[n].ptr if n else 0
@@ -57,6 +58,7 @@ def compile_stages(plan, host):
         stages.append(_stage(op=R.FX_OP_MOE_COMBINE, sync=R.FX_SYNC_GLOBAL, n_rows=d.H, n_slots=d.N_SLOTS,
                              x=B(cur), out=B(cur), aux={0: B(c.args["input"]), 1: B(c.args["weight"])},
                              layer=int(c.label.split(".")[0][1:])))
+        labels.append(c.label)
 
     for c in plan.calls:
         a = c.args
@@ -86,7 +88,9 @@ def compile_stages(plan, host):
             if a.get("amax"):
                 flags |= R.FX_F_ARGMAX | R.FX_F_HEAD
                 st.aux[3] = B(a["amax"])
+            lab = c.label
             if pend_embed is not None and a["input"] == "x_res":
+                lab = c.label + "+embed"
                 st.in_kind = R.FX_IN_EMBED
                 st.aux[0] = B("W_embed")
                 st.aux[3] = B("amax")
@@ -95,6 +99,7 @@ def compile_stages(plan, host):
                 flags |= R.FX_F_WRITE_X
                 pend_embed = None
             elif pend_combine is not None and a["input"] == "x_res":
+                lab = c.label + "+combine"
                 st.in_kind = R.FX_IN_COMBINE
                 st.x = B(cur)
                 st.aux[0] = B(pend_combine.args["input"])
@@ -115,6 +120,7 @@ def compile_stages(plan, host):
                 st.res = B(cur)
             st.flags = flags
             stages.append(st)
+            labels.append(lab)
             continue
         assert pend_embed is None, "prologue.embed must be followed by L0.qkva"
         if pend_combine is not None:
@@ -154,9 +160,11 @@ def compile_stages(plan, host):
         else:
             raise ValueError(f"unknown plan method {m}")
         stages.append(st)
+        labels.append(c.label)
     assert pend_embed is None, "a plan cannot end on prologue.embed"
     if pend_combine is not None:
         standalone_combine(pend_combine)
+    compile_stages.labels = labels
     return stages, epi, cur
 
 
@@ -174,6 +182,26 @@ class Runner:
         assert step0 + iters <= self.plan.s_max, (step0, iters, self.plan.s_max)
         self.rt.run(iters, step0, n_prompt, self.host["tokens"])
         self.last_iters = iters
+
+    def profile(self, iters, step0, n_prompt, iteration=0):
+        """Run with per-stage stamps recorded for `iteration`; returns a list of per-stage dicts:
+        label, sync, start (us from the iteration's first stamp), busy (slowest worker's share),
+        spread (last minus first worker to finish), gap (until the next stage starts)."""
+        self.rt.set_profile(iteration)
+        try:
+            self.run(iters, step0, n_prompt)
+        finally:
+            self.rt.set_profile(-1)
+        st = self.rt.read_profile(len(self.stages))[:, 8:, :].astype(np.float64) / 100.0   # workers only, us
+        t0 = st[0, :, 0].min()
+        rows = []
+        for i, lab in enumerate(self.labels):
+            start, end = st[i, :, 0].min() - t0, st[i, :, 1].max() - t0
+            nxt = st[i + 1, :, 0].min() - t0 if i + 1 < len(self.labels) else end
+            busy = (st[i, :, 1] - st[i, :, 0]).max()
+            rows.append({"label": lab, "sync": int(self.stages[i].sync), "start": start, "busy": busy,
+                         "spread": st[i, :, 1].max() - st[i, :, 1].min(), "span": end - start, "gap": nxt - end})
+        return rows
 
     def timing_us(self):
         t = self.rt.timing(self.last_iters)
@@ -214,7 +242,9 @@ def build(rt, packed, capture, meta, dims: Dims = REAL_DIMS, s_max=1056, layers=
         plan.truncate(stop_after)
     host = make_tensors(rt, plan, packed, capture, meta)
     stages, epi, x_final = compile_stages(plan, host)
-    return Runner(rt, plan, host, stages, epi, x_final)
+    runner = Runner(rt, plan, host, stages, epi, x_final)
+    runner.labels = list(compile_stages.labels)
+    return runner
 
 
 def plan_json(plan):

@@ -85,6 +85,9 @@ def lib():
         "fx_load_plan": (ctypes.c_int, [vp, ctypes.POINTER(FxStage), i32, ctypes.POINTER(FxStage), i32]),
         "fx_run": (ctypes.c_int, [vp, i32, i32, i32, vp, vp]),
         "fx_read_timing": (ctypes.c_int, [vp, ctypes.POINTER(ctypes.c_uint64), i32]),
+        "fx_last_run_ms": (ctypes.c_int, [vp, ctypes.POINTER(ctypes.c_float)]),
+        "fx_set_profile": (ctypes.c_int, [vp, i32]),
+        "fx_read_profile": (ctypes.c_int, [vp, ctypes.POINTER(ctypes.c_uint64), i32]),
         "fx_run_stage": (ctypes.c_int, [vp, ctypes.POINTER(FxStage), i32, i32, vp]),
         "fx_gen_normal_bf16": (ctypes.c_int, [vp, vp, u64, u64, u64, u64, u64, u64, ctypes.c_uint32, ctypes.c_float]),
         "fx_fill_u16": (ctypes.c_int, [vp, vp, u64, ctypes.c_uint16]),
@@ -99,7 +102,7 @@ def lib():
 
 EXPORTS = ("fx_abi_version", "fx_create", "fx_destroy", "fx_last_error", "fx_device_info", "fx_malloc", "fx_free",
            "fx_memcpy_htod", "fx_memcpy_dtoh", "fx_memcpy_dtod", "fx_memset", "fx_synchronize", "fx_load_plan",
-           "fx_run", "fx_read_timing", "fx_run_stage", "fx_gen_normal_bf16", "fx_fill_u16")
+           "fx_run", "fx_last_run_ms", "fx_set_profile", "fx_read_profile", "fx_read_timing", "fx_run_stage", "fx_gen_normal_bf16", "fx_fill_u16")
 
 
 class Runtime:
@@ -151,6 +154,25 @@ class Runtime:
 
     def run(self, iters, step0, n_prompt, tokens):
         self.check(self.L.fx_run(self.h, iters, step0, n_prompt, tokens.ptr, None), "fx_run")
+
+    def last_run_ms(self):
+        """HIP-event milliseconds of the last fx_run launch (events on the launch stream)."""
+        ms = ctypes.c_float()
+        self.check(self.L.fx_last_run_ms(self.h, ctypes.byref(ms)), "fx_last_run_ms")
+        return ms.value
+
+    def set_profile(self, iteration):
+        """Record per-stage, per-worker stamps of `iteration` in the next run (-1: off)."""
+        self.check(self.L.fx_set_profile(self.h, iteration), "fx_set_profile")
+
+    def read_profile(self, n_stages):
+        """[n_stages, 256, 2] s_memrealtime stamps (100 MHz) of the profiled iteration."""
+        n = n_stages * 256 * 2
+        buf = (ctypes.c_uint64 * n)()
+        m = self.L.fx_read_profile(self.h, buf, n)
+        if m != n:
+            raise FxError(f"fx_read_profile returned {m} of {n}")
+        return np.array(buf, np.uint64).reshape(n_stages, 256, 2)
 
     def timing(self, n):
         buf = (ctypes.c_uint64 * (n + 1))()

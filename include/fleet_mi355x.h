@@ -147,6 +147,18 @@ int fx_load_plan(fx_ctx* ctx, const fx_stage* stages, int32_t n_stages, const fx
  * the head's argmax is stored to tokens[step0 + i + 1]. stream: a hipStream_t or NULL. */
 int fx_run(fx_ctx* ctx, int32_t iters, int32_t step0, int32_t n_prompt, int64_t* tokens, void* stream);
 
+/* Elapsed milliseconds of the last fx_run's persistent launch, from HIP events recorded on the
+ * launch stream immediately before and after it. */
+int fx_last_run_ms(fx_ctx* ctx, float* ms);
+
+/* Per-stage event timing of one iteration (the reference's MPK_EVENT_TIMING + measure.py per-op
+ * gaps, docs/fleet/03-runtime.md:367-371): when iter >= 0, the next fx_run records for iteration
+ * `iter` and every worker two s_memrealtime stamps per stage, [stage][block][start, end], start when
+ * the worker begins the stage (after the previous sync), end when its share is done (before the sync).
+ * fx_read_profile copies n_stages * 256 * 2 stamps; returns the count written. */
+int fx_set_profile(fx_ctx* ctx, int32_t iter);
+int fx_read_profile(fx_ctx* ctx, uint64_t* buf, int32_t n);
+
 /* Per-iteration timestamps of the last fx_run (s_memrealtime, 100 MHz): buf[0] at the start of
  * iteration 0, buf[i] at the start of iteration i, buf[iters] at the end. Replaces the [FWD_PASS]
  * lines and event_timing.json (harness/measure.py:187-190). Returns the count written. */
