@@ -1,0 +1,133 @@
+"""Writes numpy_ref_decode.json: greedy ids, route ids and the final hidden row of a short decode
+computed by the reference's own numpy operators (harness/numpy_ref.py), composed in the
+reference's task-graph order (fleet/graph_plan.py:380-603), on the seeded synthetic weights.
+
+numpy_ref's float32 reductions go through numpy's BLAS, whose summation order is unspecified, so
+its exact bits cannot be restated; its discrete outputs (token ids, expert ids) can be pinned. This
+script is run once, in the build container where the reference is checked out, and the JSON it
+writes is the committed fixture; nothing else imports the reference.
+
+    python tests/golden/make_numpy_ref_ids.py [/path/to/reference]
+"""
+import importlib.util
+import json
+import os
+import sys
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(os.path.dirname(HERE))
+sys.path[:0] = [ROOT, os.path.join(ROOT, "fleet-amd-task_amd"), os.path.dirname(HERE)]
+
+from oracle import oracle as O          # noqa: E402  (seeded generator and bf16 helpers)
+from oracle.model import Cfg, rope_tables  # noqa: E402
+from fleet import pack_weights as P     # noqa: E402
+from fxtest import SEED, SeededCpuWeights  # noqa: E402
+
+LAYERS = 2          # layer 0 (dense MLP) and layer 1 (MoE)
+N_PROMPT = 40       # crosses the first split boundary at 32
+N_NEW = 4
+S_MAX = 64
+SPLIT = 32
+
+
+def load_numpy_ref(ref_root):
+    path = os.path.join(ref_root, "harness", "numpy_ref.py")
+    spec = importlib.util.spec_from_file_location("numpy_ref", path)
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def f32(bits):
+    return O.bf16_to_f32(np.asarray(bits, np.uint16))
+
+
+def main():
+    ref_root = sys.argv[1] if len(sys.argv) > 1 else "/root/reference"
+    nr = load_numpy_ref(ref_root)
+    c = Cfg(split=SPLIT, n_splits=S_MAX // SPLIT)
+    W = SeededCpuWeights(P.REAL_DIMS, SEED, LAYERS, head=True)
+    cos_b, sin_b = rope_tables(S_MAX, c.D_R)
+    cos, sin = f32(cos_b), f32(sin_b)
+    prompt = [int(t) for t in P.prompt_ids(SEED, N_PROMPT, c.V)]
+
+    Wf = {}
+
+    def w(key):
+        if key not in Wf:
+            Wf[key] = f32(W[key])
+        return Wf[key]
+
+    def expert(key, e):
+        return f32(W.expert(key, e))
+
+    c_kv = [np.zeros((S_MAX, c.D_C), np.float32) for _ in range(LAYERS)]
+    k_pe = [np.zeros((S_MAX, c.D_R), np.float32) for _ in range(LAYERS)]
+
+    def step_fn(token, step, head):
+        x = w("W_embed")[token].copy()
+        routes = []
+        for l in range(LAYERS):
+            _, qkva = nr.linear_norm(x, w(f"w_norm1_{l}"), w(f"W_qkva_{l}"), eps=c.eps)
+            c_row, k_row, ql, qp = nr.mla_prep(qkva, w(f"w_kv_norm_{l}"), w(f"W_uk_{l}"), cos[step], sin[step],
+                                               nh=c.NH, d_n=c.D_N, d_r=c.D_R, d_c=c.D_C, eps=c.eps)
+            c_kv[l][step] = c_row
+            k_pe[l][step] = k_row
+            partials = nr.mla_attend(ql, qp, c_kv[l], k_pe[l], step, np.float32(c.scale), split=SPLIT)
+            attn = nr.mla_merge_uv(partials, w(f"W_uv_{l}"), step, split=SPLIT)
+            x = nr.linear_residual(attn, w(f"W_o_{l}"), x)
+            if l == 0:
+                h = nr.rmsnorm(x, w("w_norm2_0"), c.eps)
+                mid = nr.linear(h, w("W_gu_0"))
+                act = nr.bf16(nr.silu(mid[:c.I_DENSE]) * mid[c.I_DENSE:])
+                x = nr.linear_residual(act, w("W_down_0"), x)
+                continue
+            h, logits, topk_w, routing, mask = nr.moe_router_norm(x, w(f"w_norm2_{l}"), w(f"W_gate_{l}"), eps=c.eps,
+                                                                   topk=c.TOPK, n_experts=c.E,
+                                                                   forced=(c.E, c.E + 1))
+            n_slots = c.TOPK + c.N_SHARED
+            ids = [int(e) for e in mask[:n_slots]]
+            # the 8 active slabs stacked in slot order with an identity mask: the same rows as
+            # indexing the whole [66, ...] tensor by mask
+            W13 = np.stack([expert(f"W13_{l}", e) for e in ids])
+            W2 = np.stack([expert(f"W2_{l}", e) for e in ids])
+            local = np.arange(n_slots + 1, dtype=np.int32)
+            local[n_slots] = n_slots
+            mid = nr.moe_w13(h, W13, local, n_slots)
+            out8 = nr.moe_w2(mid, W2, local, n_slots)
+            x = nr.moe_combine(out8, topk_w, x)
+            srt = np.sort(logits)[::-1]
+            routes.append({"ids": ids, "logits": [float(logits[e]) for e in ids[:c.TOPK]],
+                           "gap_6_7": float(srt[c.TOPK - 1] - srt[c.TOPK])})
+        if not head:
+            return None, routes, x
+        _, logits = nr.linear_norm(x, w("w_final_norm"), w("W_lm"), eps=c.eps)
+        tok = int(np.argmax(logits))
+        srt = np.sort(logits)[::-1]
+        return {"id": tok, "gap_1_2": float(srt[0] - srt[1])}, routes, x
+
+    for pos in range(N_PROMPT - 1):
+        step_fn(prompt[pos], pos, False)
+    tok = prompt[-1]
+    steps = []
+    x = None
+    for i in range(N_NEW):
+        step = N_PROMPT - 1 + i
+        t, routes, x = step_fn(tok, step, True)
+        steps.append({"step": step, "token": t["id"], "logit_gap_1_2": t["gap_1_2"], "routes": routes})
+        tok = t["id"]
+    out = {
+        "what": "greedy decode by harness/numpy_ref.py operators on seeded synthetic weights",
+        "seed": SEED, "layers": LAYERS, "prompt_len": N_PROMPT, "n_new": N_NEW, "s_max": S_MAX, "split": SPLIT,
+        "scale": c.scale, "prompt": prompt, "steps": steps,
+        "x_final_bf16": [int(v) for v in O.f32_to_bf16(x)],
+    }
+    with open(os.path.join(HERE, "numpy_ref_decode.json"), "w") as f:
+        json.dump(out, f, indent=1)
+    print(json.dumps([{k: s[k] for k in ("step", "token", "logit_gap_1_2")} for s in steps]))
+
+
+if __name__ == "__main__":
+    main()
