@@ -10,10 +10,14 @@ at batch 1. A "step" is one decoded token; `--steps` tokens are timed, starting 
 (so every timed token attends over 1,024..1,024+steps-1 positions), after `--warmup` untimed
 tokens at the same positions. Inputs are resident in HBM when the timed region starts.
 
-value        us per decoded token: HIP-event time of the timed fx_run launch / steps
+value        us per decoded token: one persistent launch per token (fx_launch, queued back to back on
+             one stream, no host wait in between); HIP events on that stream around the K launches
+             / K. Prefill runs under the kernel symbol fx_prefill, decode under fx_persistent, so a
+             kernel trace of this command averages fx_persistent over decode tokens only
 roofline     algorithmic HBM bytes per token (every weight the token touches once -- 8 of the 66
              experts per MoE layer -- plus the latent-cache rows read and the embedding row; mean
-             over the timed tokens) / us per token, against the published 8 TB/s
+             over the timed tokens) / us per token, against the published 8 TB/s; traffic = the
+             measured HBM bytes per launch from the committed rocprofv3 --pmc summary
 cpu_baseline the CPU oracle (oracle/, a C port of harness/numpy_ref.py semantics, OpenMP) decoding
              the first `--cpu-tokens` tokens of the same run on this host's cores, checked for
              equal ids; weights it touches are copied to host memory before its timed region
@@ -44,6 +48,17 @@ METRIC = "µs/decoded token (batch 1, ctx 1024) and % of HBM roofline on 1 MI355
 
 def log(*a):
     print("[bench]", *a, file=sys.stderr, flush=True)
+
+
+def traffic_bytes(ctx):
+    """HBM bytes per fx_persistent dispatch from the committed rocprofv3 --pmc summary (FETCH_SIZE and
+    WRITE_SIZE, each scaled by the same counter's reading on a copy kernel of known size), or None.
+    Counters cannot be read inside this process, so the figure comes from the profile runs."""
+    f = ROOT / "profiles" / "fx_persistent_decode_ctx1024_traffic.json"
+    if ctx != 1024 or not f.exists():
+        return None
+    t = json.loads(f.read_text())
+    return int(t["bytes_per_dispatch"])
 
 
 def cpu_baseline(rt, runner, bufs, plan, prompt, ctx, n_tok, gpu_ids):
@@ -139,20 +154,27 @@ def main():
     runner.run(ctx - 1, 0, ctx)
     prefill_s = time.time() - t0
     log(f"prefill of {ctx - 1} positions: {prefill_s:.2f} s ({1e6 * prefill_s / (ctx - 1):.0f} us/position, head skipped)")
+    assert K + 1 <= R.FX_MAX_MARKS, "at most 255 timed tokens"
+    for i in range(Wm):
+        runner.launch(1, ctx - 1 + i, ctx)
+    runner.finish()
     if Wm > 0:
-        runner.run(Wm, ctx - 1, ctx)
-        log(f"warmup: {Wm} tokens, {1e3 * rt.last_run_ms() / Wm:.1f} us/token")
+        log(f"warmup: {Wm} tokens")
     t0 = time.perf_counter()
-    runner.run(K, ctx - 1, ctx)
+    rt.mark(0)
+    for i in range(K):
+        runner.launch(1, ctx - 1 + i, ctx)
+        rt.mark(i + 1)
+    runner.finish()
     wall_ms = 1e3 * (time.perf_counter() - t0)
-    ev_ms = rt.last_run_ms()
-    iter_us = runner.timing_us()
-    us_tok = 1e3 * ev_ms / K
+    per_launch = [1e3 * rt.marks_ms(i, i + 1) for i in range(K)]
+    us_tok = 1e3 * rt.marks_ms(0, K) / K
     ids = runner.host["tokens"].download()[ctx:ctx + K].tolist()
     mean_bytes = sum(P.bytes_per_token(d, ctx + i) for i in range(K)) / K
     achieved = mean_bytes / (us_tok * 1e-6) / 1e9
-    log(f"decode: {us_tok:.1f} us/token (event), wall {wall_ms / K * 1e3:.1f} us/token, iteration median "
-        f"{statistics.median(iter_us):.1f} us; {achieved:.0f} GB/s = {100 * achieved / HBM_PEAK_GBPS:.1f}% of 8 TB/s")
+    log(f"decode: {us_tok:.1f} us/token (events), wall {wall_ms / K * 1e3:.1f} us/token, per-launch median "
+        f"{statistics.median(per_launch):.1f} min {min(per_launch):.1f} max {max(per_launch):.1f} us; "
+        f"{achieved:.0f} GB/s = {100 * achieved / HBM_PEAK_GBPS:.1f}% of 8 TB/s")
     log(f"ids {ids}")
     out = {
         "metric": METRIC, "value": round(us_tok, 2), "unit": "µs/token", "n_gpus": 1, "steps": K, "warmup": Wm,
@@ -162,9 +184,9 @@ def main():
                                "greedy decode at batch 1", "layers": d.L, "batch": 1, "ctx": ctx, "decode_tokens": K,
                    "splits": plan.n_splits, "seed": args.seed},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic_bytes(ctx),
                      "bytes_per_token": int(mean_bytes), "kernel": "fx_persistent"},
-        "iter_us_median": round(statistics.median(iter_us), 2), "prefill_s": round(prefill_s, 2),
+        "launch_us_median": round(statistics.median(per_launch), 2), "prefill_s": round(prefill_s, 2),
         "ids": ids,
     }
     if not args.no_cpu_baseline:

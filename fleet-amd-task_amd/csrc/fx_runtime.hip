@@ -89,7 +89,7 @@ __device__ __forceinline__ void scheduler_sync(uint32_t* sync, int x, uint32_t e
   if (lane < FX_XWORKERS) flag_st(&sync[FX_FLAG_GO(wb)], epoch);
 }
 
-__global__ void __launch_bounds__(FX_THREADS) fx_persistent(FxRunArgs a) {
+__device__ __forceinline__ void persistent_body(const FxRunArgs& a) {
   extern __shared__ __attribute__((aligned(16))) char lds[];
   const int b = blockIdx.x;
   const int x = b & 7, rank = b >> 3;
@@ -155,6 +155,12 @@ __global__ void __launch_bounds__(FX_THREADS) fx_persistent(FxRunArgs a) {
   }
   if (env.worker == 0 && threadIdx.x == 0 && a.timing) a.timing[a.iters] = __builtin_amdgcn_s_memrealtime();
 }
+
+// The decode launch (iterations that end in the LM head + argmax) and the prefill launch (prompt
+// positions only: the head stages are skipped) run the same body; they are two symbols so that a
+// kernel trace attributes prefill and decode time separately.
+__global__ void __launch_bounds__(FX_THREADS) fx_persistent(FxRunArgs a) { persistent_body(a); }
+__global__ void __launch_bounds__(FX_THREADS) fx_prefill(FxRunArgs a) { persistent_body(a); }
 
 // one stage as a standalone launch (kernel suite): same work split, no syncs
 __global__ void __launch_bounds__(FX_THREADS) fx_stage_kernel(fx_stage st, int step, int iter, int n_prompt,
@@ -305,6 +311,7 @@ struct fx_ctx {
   int n_epi = 0;
   std::vector<fx_stage> h_stages, h_epi;
   hipEvent_t ev0 = nullptr, ev1 = nullptr;
+  hipEvent_t marks[FX_MAX_MARKS] = {};
   uint64_t* prof = nullptr;
   size_t prof_words = 0;
   int prof_iter = -1;
@@ -344,10 +351,15 @@ int fx_create(int device, fx_ctx** out) {
   }
   *out = c;
   HIPCHK(c, hipFuncSetAttribute((const void*)fx_persistent, hipFuncAttributeMaxDynamicSharedMemorySize, FX_LDS_BYTES));
+  HIPCHK(c, hipFuncSetAttribute((const void*)fx_prefill, hipFuncAttributeMaxDynamicSharedMemorySize, FX_LDS_BYTES));
   HIPCHK(c, hipFuncSetAttribute((const void*)fx_stage_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, FX_LDS_BYTES));
   HIPCHK(c, hipFuncSetAttribute((const void*)fx_xcc_map, hipFuncAttributeMaxDynamicSharedMemorySize, FX_LDS_BYTES));
   HIPCHK(c, hipMalloc(&c->sync, FX_SYNC_WORDS * 4));
   HIPCHK(c, hipMemset(c->sync, 0, FX_SYNC_WORDS * 4));
+  c->timing_cap = FX_MAX_ITERS + 1;
+  HIPCHK(c, hipMalloc(&c->timing, sizeof(uint64_t) * c->timing_cap));
+  HIPCHK(c, hipEventCreate(&c->ev0));
+  HIPCHK(c, hipEventCreate(&c->ev1));
   // the work split assumes block b runs on XCD b % 8 (round-robin dispatch); verify it once
   uint32_t* d = nullptr;
   HIPCHK(c, hipMalloc(&d, FX_BLOCKS * 4));
@@ -370,6 +382,8 @@ int fx_destroy(fx_ctx* c) {
   if (c->d_epi) (void)hipFree(c->d_epi);
   if (c->ev0) (void)hipEventDestroy(c->ev0);
   if (c->ev1) (void)hipEventDestroy(c->ev1);
+  for (hipEvent_t e : c->marks)
+    if (e) (void)hipEventDestroy(e);
   if (c->prof) (void)hipFree(c->prof);
   delete c;
   return FX_OK;
@@ -503,30 +517,25 @@ int fx_load_plan(fx_ctx* c, const fx_stage* st, int32_t n, const fx_stage* epi, 
   return FX_OK;
 }
 
-int fx_run(fx_ctx* c, int32_t iters, int32_t step0, int32_t n_prompt, int64_t* tokens, void* stream) {
+int fx_launch(fx_ctx* c, int32_t iters, int32_t step0, int32_t n_prompt, int64_t* tokens, void* stream) {
   if (!c) return FX_E_ARG;
   if (!c->d_stages) return fail(c, FX_E_STATE, "no plan loaded");
-  if (iters <= 0 || step0 < 0 || !tokens) return fail(c, FX_E_ARG, "iters/step0/tokens");
+  if (iters <= 0 || iters > FX_MAX_ITERS || step0 < 0 || !tokens) return fail(c, FX_E_ARG, "iters/step0/tokens");
   for (const fx_stage& s : c->h_stages) {
     if (s.s_max > 0 && step0 + iters > s.s_max) return fail(c, FX_E_ARG, "steps exceed the cache length s_max");
-  }
-  if (c->timing_cap < iters + 1) {
-    if (c->timing) HIPCHK(c, hipFree(c->timing));
-    c->timing_cap = iters + 1;
-    HIPCHK(c, hipMalloc(&c->timing, sizeof(uint64_t) * c->timing_cap));
   }
   int syncs = 0;
   for (const fx_stage& s : c->h_stages) syncs += s.sync != FX_SYNC_NONE;
   int syncs_epi = 0;
   for (const fx_stage& s : c->h_epi) syncs_epi += s.sync != FX_SYNC_NONE;
   const uint64_t total = (uint64_t)syncs * iters + syncs_epi;
+  hipStream_t s = (hipStream_t)stream;
   if ((uint64_t)c->epoch + total > 0xF0000000ull) {
+    // flags restart from zero: wait for every launch still using them
+    HIPCHK(c, hipStreamSynchronize(s));
     HIPCHK(c, hipMemset(c->sync, 0, FX_SYNC_WORDS * 4));
     c->epoch = 0;
   }
-  uint32_t err = 0;
-  HIPCHK(c, hipMemcpy(&err, c->sync + FX_FLAG_ERROR, 4, hipMemcpyDeviceToHost));
-  if (err) return fail(c, FX_E_STATE, "a previous run timed out; create a new context");
   FxRunArgs a;
   a.stages = c->d_stages;
   a.n_stages = c->n_stages;
@@ -543,29 +552,54 @@ int fx_run(fx_ctx* c, int32_t iters, int32_t step0, int32_t n_prompt, int64_t* t
   if (c->prof_iter >= 0 && c->prof_iter < iters) {
     const size_t words = (size_t)c->n_stages * FX_BLOCKS * 2;
     if (c->prof_words < words) {
+      HIPCHK(c, hipStreamSynchronize(s));
       if (c->prof) HIPCHK(c, hipFree(c->prof));
       HIPCHK(c, hipMalloc(&c->prof, words * 8));
       c->prof_words = words;
     }
-    HIPCHK(c, hipMemset(c->prof, 0, words * 8));
+    HIPCHK(c, hipMemsetAsync(c->prof, 0, words * 8, s));
     a.prof = c->prof;
     a.prof_iter = c->prof_iter;
   }
   a.epoch0 = c->epoch;
   void* args[] = {&a};
-  hipStream_t s = (hipStream_t)stream;
-  if (!c->ev0) {
-    HIPCHK(c, hipEventCreate(&c->ev0));
-    HIPCHK(c, hipEventCreate(&c->ev1));
-  }
+  // every iteration skips the head (all positions inside the prompt): the prefill symbol
+  const bool prefill = (int64_t)step0 + iters < (int64_t)n_prompt;
+  const void* fn = prefill ? (const void*)fx_prefill : (const void*)fx_persistent;
   HIPCHK(c, hipEventRecord(c->ev0, s));
-  HIPCHK(c, hipLaunchCooperativeKernel((const void*)fx_persistent, dim3(FX_BLOCKS), dim3(FX_THREADS), args, FX_LDS_BYTES, s));
+  HIPCHK(c, hipLaunchCooperativeKernel(fn, dim3(FX_BLOCKS), dim3(FX_THREADS), args, FX_LDS_BYTES, s));
   HIPCHK(c, hipEventRecord(c->ev1, s));
   c->epoch += (uint32_t)total;
   c->last_iters = iters;
-  HIPCHK(c, hipStreamSynchronize(s));
+  return FX_OK;
+}
+
+int fx_finish(fx_ctx* c, void* stream) {
+  if (!c) return FX_E_ARG;
+  HIPCHK(c, hipStreamSynchronize((hipStream_t)stream));
+  uint32_t err = 0;
   HIPCHK(c, hipMemcpy(&err, c->sync + FX_FLAG_ERROR, 4, hipMemcpyDeviceToHost));
-  if (err) return fail(c, FX_E_STATE, "a synchronisation wait timed out inside the persistent kernel");
+  if (err) return fail(c, FX_E_STATE, "a synchronisation wait timed out inside the persistent kernel; create a new context");
+  return FX_OK;
+}
+
+int fx_run(fx_ctx* c, int32_t iters, int32_t step0, int32_t n_prompt, int64_t* tokens, void* stream) {
+  const int r = fx_launch(c, iters, step0, n_prompt, tokens, stream);
+  if (r) return r;
+  return fx_finish(c, stream);
+}
+
+int fx_mark(fx_ctx* c, int32_t idx, void* stream) {
+  if (!c || idx < 0 || idx >= FX_MAX_MARKS) return fail(c, FX_E_ARG, "mark index");
+  if (!c->marks[idx]) HIPCHK(c, hipEventCreate(&c->marks[idx]));
+  HIPCHK(c, hipEventRecord(c->marks[idx], (hipStream_t)stream));
+  return FX_OK;
+}
+
+int fx_marks_ms(fx_ctx* c, int32_t i, int32_t j, float* ms) {
+  if (!c || !ms || i < 0 || j < 0 || i >= FX_MAX_MARKS || j >= FX_MAX_MARKS || !c->marks[i] || !c->marks[j])
+    return fail(c, FX_E_ARG, "mark index");
+  HIPCHK(c, hipEventElapsedTime(ms, c->marks[i], c->marks[j]));
   return FX_OK;
 }
 
@@ -586,7 +620,7 @@ int fx_read_profile(fx_ctx* c, uint64_t* buf, int32_t n) {
 
 int fx_last_run_ms(fx_ctx* c, float* ms) {
   if (!c || !ms) return FX_E_ARG;
-  if (!c->ev0) return fail(c, FX_E_STATE, "no run yet");
+  if (!c->last_iters) return fail(c, FX_E_STATE, "no run yet");
   HIPCHK(c, hipEventElapsedTime(ms, c->ev0, c->ev1));
   return FX_OK;
 }

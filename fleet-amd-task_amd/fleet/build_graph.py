@@ -183,6 +183,15 @@ class Runner:
         self.rt.run(iters, step0, n_prompt, self.host["tokens"])
         self.last_iters = iters
 
+    def launch(self, iters, step0, n_prompt):
+        """Enqueue `iters` iterations as one launch without waiting (fx_launch); finish() waits."""
+        assert step0 + iters <= self.plan.s_max, (step0, iters, self.plan.s_max)
+        self.rt.launch(iters, step0, n_prompt, self.host["tokens"])
+        self.last_iters = iters
+
+    def finish(self):
+        self.rt.finish()
+
     def profile(self, iters, step0, n_prompt, iteration=0):
         """Run with per-stage stamps recorded for `iteration`; returns a list of per-stage dicts:
         label, sync, start (us from the iteration's first stamp), busy (slowest worker's share),

@@ -23,6 +23,8 @@ FX_OP_DENSE_GU, FX_OP_ARGMAX = 9, 10
 FX_IN_VEC, FX_IN_EMBED, FX_IN_COMBINE = 0, 1, 2
 FX_F_NORM, FX_F_RESIDUAL, FX_F_WRITE_X, FX_F_ARGMAX, FX_F_HEAD = 1, 2, 4, 8, 16
 FX_SYNC_NONE, FX_SYNC_XCD, FX_SYNC_GLOBAL = 0, 1, 2
+FX_MAX_ITERS, FX_MAX_MARKS = 65536, 256
+FX_ABI_VERSION = 2
 WORKERS = 248          # 256 CUs minus one scheduler workgroup per XCD
 XCDS = 8
 
@@ -84,6 +86,10 @@ def lib():
         "fx_synchronize": (ctypes.c_int, [vp]),
         "fx_load_plan": (ctypes.c_int, [vp, ctypes.POINTER(FxStage), i32, ctypes.POINTER(FxStage), i32]),
         "fx_run": (ctypes.c_int, [vp, i32, i32, i32, vp, vp]),
+        "fx_launch": (ctypes.c_int, [vp, i32, i32, i32, vp, vp]),
+        "fx_finish": (ctypes.c_int, [vp, vp]),
+        "fx_mark": (ctypes.c_int, [vp, i32, vp]),
+        "fx_marks_ms": (ctypes.c_int, [vp, i32, i32, ctypes.POINTER(ctypes.c_float)]),
         "fx_read_timing": (ctypes.c_int, [vp, ctypes.POINTER(ctypes.c_uint64), i32]),
         "fx_last_run_ms": (ctypes.c_int, [vp, ctypes.POINTER(ctypes.c_float)]),
         "fx_set_profile": (ctypes.c_int, [vp, i32]),
@@ -102,7 +108,8 @@ def lib():
 
 EXPORTS = ("fx_abi_version", "fx_create", "fx_destroy", "fx_last_error", "fx_device_info", "fx_malloc", "fx_free",
            "fx_memcpy_htod", "fx_memcpy_dtoh", "fx_memcpy_dtod", "fx_memset", "fx_synchronize", "fx_load_plan",
-           "fx_run", "fx_last_run_ms", "fx_set_profile", "fx_read_profile", "fx_read_timing", "fx_run_stage", "fx_gen_normal_bf16", "fx_fill_u16")
+           "fx_run", "fx_launch", "fx_finish", "fx_mark", "fx_marks_ms", "fx_last_run_ms", "fx_set_profile",
+           "fx_read_profile", "fx_read_timing", "fx_run_stage", "fx_gen_normal_bf16", "fx_fill_u16")
 
 
 class Runtime:
@@ -110,6 +117,9 @@ class Runtime:
 
     def __init__(self, device=0):
         self.L = lib()
+        v = self.L.fx_abi_version()
+        if v != FX_ABI_VERSION:
+            raise FxError(f"libfleet_mi355x ABI {v}, this module expects {FX_ABI_VERSION}: rebuild the library")
         h = ctypes.c_void_p()
         rc = self.L.fx_create(device, ctypes.byref(h))
         self.h = h
@@ -154,6 +164,21 @@ class Runtime:
 
     def run(self, iters, step0, n_prompt, tokens):
         self.check(self.L.fx_run(self.h, iters, step0, n_prompt, tokens.ptr, None), "fx_run")
+
+    def launch(self, iters, step0, n_prompt, tokens):
+        """Enqueue one persistent launch (no host wait); finish() waits and checks."""
+        self.check(self.L.fx_launch(self.h, iters, step0, n_prompt, tokens.ptr, None), "fx_launch")
+
+    def finish(self):
+        self.check(self.L.fx_finish(self.h, None), "fx_finish")
+
+    def mark(self, idx):
+        self.check(self.L.fx_mark(self.h, idx, None), "fx_mark")
+
+    def marks_ms(self, i, j):
+        ms = ctypes.c_float()
+        self.check(self.L.fx_marks_ms(self.h, i, j, ctypes.byref(ms)), "fx_marks_ms")
+        return ms.value
 
     def last_run_ms(self):
         """HIP-event milliseconds of the last fx_run launch (events on the launch stream)."""

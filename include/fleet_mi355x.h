@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define FX_ABI_VERSION 1
+#define FX_ABI_VERSION 2
 
 /* ---- error codes ---------------------------------------------------------------------------- */
 #define FX_OK 0
@@ -147,9 +147,25 @@ int fx_load_plan(fx_ctx* ctx, const fx_stage* stages, int32_t n_stages, const fx
  * the head's argmax is stored to tokens[step0 + i + 1]. stream: a hipStream_t or NULL. */
 int fx_run(fx_ctx* ctx, int32_t iters, int32_t step0, int32_t n_prompt, int64_t* tokens, void* stream);
 
-/* Elapsed milliseconds of the last fx_run's persistent launch, from HIP events recorded on the
- * launch stream immediately before and after it. */
+/* fx_run in two halves, so that launches can be queued back to back: fx_launch enqueues the
+ * persistent launch on `stream` and returns (no host wait); fx_finish waits for the stream and
+ * reports a wait that timed out inside any launch since the last fx_finish. fx_run = both. A launch
+ * whose iterations all lie inside the prompt (step0 + iters < n_prompt: the head never runs) uses
+ * the kernel symbol fx_prefill, every other launch fx_persistent (the same code). iters is at most
+ * FX_MAX_ITERS. */
+#define FX_MAX_ITERS 65536
+int fx_launch(fx_ctx* ctx, int32_t iters, int32_t step0, int32_t n_prompt, int64_t* tokens, void* stream);
+int fx_finish(fx_ctx* ctx, void* stream);
+
+/* Elapsed milliseconds of the last launch, from HIP events recorded on the launch stream
+ * immediately before and after it (valid once that launch has finished). */
 int fx_last_run_ms(fx_ctx* ctx, float* ms);
+
+/* Timing marks: fx_mark records HIP event `idx` (0 <= idx < FX_MAX_MARKS) on `stream`;
+ * fx_marks_ms gives the milliseconds from mark i to mark j once both have completed. */
+#define FX_MAX_MARKS 256
+int fx_mark(fx_ctx* ctx, int32_t idx, void* stream);
+int fx_marks_ms(fx_ctx* ctx, int32_t i, int32_t j, float* ms);
 
 /* Per-stage event timing of one iteration (the reference's MPK_EVENT_TIMING + measure.py per-op
  * gaps, docs/fleet/03-runtime.md:367-371): when iter >= 0, the next fx_run records for iteration
