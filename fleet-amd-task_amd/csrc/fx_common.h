@@ -1,37 +1,45 @@
-// Per-workgroup state, sync-area and LDS layouts shared by the operators and the runtime.
+// Per-workgroup state, packet tags and the LDS layout shared by the operators and the runtime.
 #pragma once
 #include "fx_device.h"
 #include "../../include/fleet_mi355x.h"
 
-// Work split: 248 workers = 256 CUs minus one scheduler per XCD; worker w sits on XCD w % 8 and is
-// rank w / 8 of the 31 workers of its XCD.
+// 256 workers, one per CU: worker w runs on XCD w % 8 and is rank w / 8 of the 32 of its XCD.
+#define FX_WORKERS 256
+#define FX_XWORKERS 32
+
 struct FxEnv {
   int worker, nworkers;   // global worker index and count
   int xcd, xrank, xworkers;
   int step, iter;
   int n_prompt;
-  int moe_e;              // expert of this XCD's slot chosen by the last MOE_W13 stage (-1: unknown)
+  uint32_t tbase;         // tag base of this iteration: epoch0 + iter * n_stages
+  int sidx;               // index of the running stage in the table
+  int64_t token;          // token of this iteration (set by the embed prologue; -1 before)
   int64_t* tokens;
-  uint32_t* sync;         // runtime sync area (flags + counters)
+  uint32_t* err;          // the run's error flag
+  uint64_t* pst;          // profile stamps of this stage and worker, or null
   char* lds;
 };
 
-// sync area layout (uint32 index, one 128-byte line per flag)
-#define FX_FLAG_ARRIVE(b) ((b) * 32)
-#define FX_FLAG_GO(b) ((256 + (b)) * 32)
-#define FX_FLAG_XCD(x) ((512 + (x)) * 32)
-#define FX_CNT_ATTEND(x) ((520 + (x)) * 32)
-#define FX_FLAG_ERROR (528 * 32)
-#define FX_SYNC_WORDS (529 * 32)
+// tag that packet input k of stage s carries / that this stage's outputs carry
+__device__ __forceinline__ uint32_t tag_in(const fx_stage& s, const FxEnv& e, int k) {
+  return e.tbase + (uint32_t)(s.src[k] + 1);
+}
+__device__ __forceinline__ uint32_t tag_out(const FxEnv& e) { return e.tbase + (uint32_t)(e.sidx + 1); }
+
+// profile stamp `slot` of the running stage (thread 0 only)
+__device__ __forceinline__ void prof_mark(const FxEnv& e, int slot) {
+  if (e.pst && threadIdx.x == 0) e.pst[slot] = __builtin_amdgcn_s_memrealtime();
+}
 
 // LDS layout (bytes)
 #define LDS_XS 0                         // f32 [11264]  GEMV input row
 #define LDS_RED (45056)                  // f32 [1024]   reductions / small tables
-#define LDS_MISC (LDS_RED + 4096)        // scalars: token, expert, slot weights, residual rows
-#define LDS_RES (LDS_MISC + 512)         // f32 [64]     residual values of the worker's rows
+#define LDS_MISC (LDS_RED + 4096)        // scalars: token, expert, slot weights
+#define LDS_RES (LDS_MISC + 512)         // f32 [128]    residual / output values of the worker's rows
 #define LDS_TILE (LDS_MISC + 1024)       // attention tile / merge tables (<= 37.5 KiB)
 #define LDS_STAGE (FX_LDS_BYTES - 256)   // the current fx_stage (persistent kernel)
-#define FX_MAX_RES_ROWS 64
+#define FX_MAX_OUT_ROWS 128
 
 __device__ __forceinline__ void range_split(int n, int parts, int i, int& lo, int& hi) {
   lo = (int)(((long long)n * i) / parts);

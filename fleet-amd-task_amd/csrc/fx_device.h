@@ -22,6 +22,7 @@
 #define FX_WAVES 4
 #define FX_XCDS 8
 #define FX_LDS_BYTES (96 * 1024)
+#define FX_TIMEOUT_TICKS (200ull * 1000 * 1000)   // 2 s of s_memrealtime: a wait this long fails the run
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
@@ -127,6 +128,98 @@ __device__ __forceinline__ void flag_st(uint32_t* p, uint32_t v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ void wait_mem() { __builtin_amdgcn_s_waitcnt(0); }
+
+// ------------------------------------------------------------------------------------------------
+// packets: 8 bytes = 32-bit payload | 32-bit tag of the producing stage. Stored and loaded with
+// sc1, two packets per 16-byte access (the tag of each packet is checked on its own).
+
+__device__ __forceinline__ void pk_put(void* base, uint32_t pkt, uint32_t payload, uint32_t tag) {
+  u32x2 v;
+  v.x = payload;
+  v.y = tag;
+  stc8(base, pkt * 8u, v);
+}
+// packets pkt, pkt + 1 (pkt even)
+__device__ __forceinline__ void pk_put2(void* base, uint32_t pkt, uint32_t p0, uint32_t p1, uint32_t tag) {
+  u32x4 v;
+  v.x = p0;
+  v.y = tag;
+  v.z = p1;
+  v.w = tag;
+  stc16(base, pkt * 8u, v);
+}
+
+// Wait until packets pkt, pkt + 1 (pkt even) carry `tag`; returns them (payloads in .x, .z).
+// Gives up after FX_TIMEOUT_TICKS and raises the run's error flag; once the flag is up every wait
+// returns at once, so the grid drains.
+__device__ __forceinline__ u32x4 pk_wait2(const void* base, uint32_t pkt, uint32_t tag, uint32_t* err) {
+  u32x4 v = ldc16(base, pkt * 8u);
+  if (v.y == tag && v.w == tag) return v;
+  const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+  for (uint32_t spin = 1;; ++spin) {
+    __builtin_amdgcn_s_sleep(1);
+    v = ldc16(base, pkt * 8u);
+    if (v.y == tag && v.w == tag) break;
+    if ((spin & 63u) == 0) {
+      if (__builtin_amdgcn_s_memrealtime() - t0 > FX_TIMEOUT_TICKS) {
+        __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        break;
+      }
+      if (__hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) break;
+    }
+  }
+  return v;
+}
+// Poll the packet pairs q = first + n * stride (n < N, q < npairs; pair q = packets 2q, 2q + 1)
+// until each carries `tag`; out[n] receives pair n (payloads in .x, .z). Every round issues the
+// loads of all pending pairs before checking any of them.
+template <int N>
+__device__ __forceinline__ void pk_wait_pairs(const void* base, int first, int stride, int npairs, uint32_t tag,
+                                              uint32_t* err, u32x4* out) {
+  uint32_t pending = 0;
+#pragma unroll
+  for (int n = 0; n < N; ++n)
+    if (first + n * stride < npairs) pending |= 1u << n;
+  uint64_t t0 = 0;
+  for (uint32_t round = 0; pending != 0u; ++round) {
+#pragma unroll
+    for (int n = 0; n < N; ++n)
+      if (pending & (1u << n)) out[n] = ldc16(base, (uint32_t)(first + n * stride) * 16u);
+#pragma unroll
+    for (int n = 0; n < N; ++n)
+      if ((pending & (1u << n)) && out[n].y == tag && out[n].w == tag) pending &= ~(1u << n);
+    if (pending == 0u) break;
+    if (round == 0) t0 = __builtin_amdgcn_s_memrealtime();
+    __builtin_amdgcn_s_sleep(1);
+    if ((round & 15u) == 15u) {
+      if (__builtin_amdgcn_s_memrealtime() - t0 > FX_TIMEOUT_TICKS) {
+        __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        break;
+      }
+      if (__hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) break;
+    }
+  }
+}
+
+// one packet (any index): payload
+__device__ __forceinline__ uint32_t pk_wait1(const void* base, uint32_t pkt, uint32_t tag, uint32_t* err) {
+  u32x2 v = ldc8(base, pkt * 8u);
+  if (v.y == tag) return v.x;
+  const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+  for (uint32_t spin = 1;; ++spin) {
+    __builtin_amdgcn_s_sleep(1);
+    v = ldc8(base, pkt * 8u);
+    if (v.y == tag) break;
+    if ((spin & 63u) == 0) {
+      if (__builtin_amdgcn_s_memrealtime() - t0 > FX_TIMEOUT_TICKS) {
+        __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        break;
+      }
+      if (__hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) break;
+    }
+  }
+  return v.x;
+}
 
 // weights: read-only for the whole dispatch, streamed once -> non-temporal 16-byte loads
 __device__ __forceinline__ u32x4 ldw16(const void* p) { return __builtin_nontemporal_load((const u32x4*)p); }

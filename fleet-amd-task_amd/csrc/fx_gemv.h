@@ -69,24 +69,30 @@ __device__ __forceinline__ void gemv_prime(Tile<R, NJ>& t0, const uint16_t* W, i
 
 // Walk the wave's groups g = wave, wave + 4, ...; t0 holds group `wave` (gemv_prime). emit(g, rows,
 // acc) sees the R results on every lane (row < 0: no row).
-template <int R, int NJ, class RowFn, class EmitFn>
-__device__ __forceinline__ void gemv_pipe(Tile<R, NJ>& t0, const uint16_t* W, int K, const float* xs, int ngroups,
-                                          RowFn& rowof, EmitFn emit) {
+template <int R, int NJ, class RowFn, class XsFn, class EmitFn>
+__device__ __forceinline__ void gemv_pipe_x(Tile<R, NJ>& t0, const uint16_t* W, int K, XsFn xsof, int ngroups,
+                                            RowFn& rowof, EmitFn emit) {
   Tile<R, NJ> t1;
   float acc[R];
   int g = wave_id();
   while (g < ngroups) {
     const int g1 = g + FX_WAVES;
     if (g1 < ngroups) tile_load(t1, W, K, g1, rowof);
-    tile_dot(t0, xs, K, acc);
+    tile_dot(t0, xsof(g), K, acc);
     emit(g, t0.row, acc);
     if (g1 >= ngroups) break;
     const int g2 = g1 + FX_WAVES;
     if (g2 < ngroups) tile_load(t0, W, K, g2, rowof);
-    tile_dot(t1, xs, K, acc);
+    tile_dot(t1, xsof(g1), K, acc);
     emit(g1, t1.row, acc);
     g = g2;
   }
+}
+// the same walk with one input row for every group
+template <int R, int NJ, class RowFn, class EmitFn>
+__device__ __forceinline__ void gemv_pipe(Tile<R, NJ>& t0, const uint16_t* W, int K, const float* xs, int ngroups,
+                                          RowFn& rowof, EmitFn emit) {
+  gemv_pipe_x(t0, W, K, [=](int) { return xs; }, ngroups, rowof, emit);
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -97,10 +103,32 @@ __device__ __forceinline__ void unpack8(u32x4 v, float* d) {
   d[4] = bf_lo(v.z); d[5] = bf_hi(v.z); d[6] = bf_lo(v.w); d[7] = bf_hi(v.w);
 }
 
-__device__ __forceinline__ void load_vec_sc1(float* xs, const void* src, int K) {
-  for (int i = threadIdx.x * 8; i < K; i += FX_THREADS * 8) unpack8(ldc16(src, (uint32_t)i * 2), xs + i);
+// xs[0, K) <- the K bf16 values of a packet vector (K / 2 packets, K a multiple of 4): thread t
+// takes pairs t, t + 256, ... (4 values each). Ends before any __syncthreads: the caller syncs.
+template <int N>
+__device__ __forceinline__ void poll_row_n(float* xs, const void* src, int K, uint32_t tag, uint32_t* err) {
+  u32x4 v[N];
+  const int npairs = K >> 2;
+  pk_wait_pairs<N>(src, threadIdx.x, FX_THREADS, npairs, tag, err, v);
+#pragma unroll
+  for (int n = 0; n < N; ++n) {
+    const int q = threadIdx.x + n * FX_THREADS;
+    if (q < npairs) {
+      xs[4 * q + 0] = bf_lo(v[n].x);
+      xs[4 * q + 1] = bf_hi(v[n].x);
+      xs[4 * q + 2] = bf_lo(v[n].z);
+      xs[4 * q + 3] = bf_hi(v[n].z);
+    }
+  }
+}
+__device__ __forceinline__ void poll_row(float* xs, const void* src, int K, uint32_t tag, uint32_t* err) {
+  if (K <= 4 * FX_THREADS) poll_row_n<1>(xs, src, K, tag, err);
+  else if (K <= 8 * FX_THREADS) poll_row_n<2>(xs, src, K, tag, err);
+  else if (K <= 16 * FX_THREADS) poll_row_n<4>(xs, src, K, tag, err);
+  else poll_row_n<12>(xs, src, K, tag, err);
 }
 
+// plain (non-packet) copy of a bf16 row to a dump buffer
 __device__ __forceinline__ void store_vec_sc1(void* dst, const float* xs, int K) {
   for (int i = threadIdx.x * 8; i < K; i += FX_THREADS * 8) {
     u32x4 v;
@@ -110,36 +138,6 @@ __device__ __forceinline__ void store_vec_sc1(void* dst, const float* xs, int K)
     v.w = pack2(xs[i + 6], xs[i + 7]);
     stc16(dst, (uint32_t)i * 2, v);
   }
-}
-
-// x + sum_s out8[s] * topk_w[s] for the 8 slots in slot order, mul then add, one bf16 rounding
-// (harness/numpy_ref.py:316-321). All nine rows' chunks are loaded before any arithmetic.
-#define FX_SLOTS 8
-__device__ __forceinline__ void combine_chunk(const void* x, const void* out8, const float* w, int K, int i, float* dst) {
-  u32x4 v = ldc16(x, (uint32_t)i * 2);
-  u32x4 o[FX_SLOTS];
-#pragma unroll
-  for (int s = 0; s < FX_SLOTS; ++s) o[s] = ldc16(out8, (uint32_t)(s * K + i) * 2);
-  float acc[8];
-  unpack8(v, acc);
-#pragma unroll
-  for (int s = 0; s < FX_SLOTS; ++s) {
-    float ov[8];
-    unpack8(o[s], ov);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      float t = ov[e] * w[s];
-      acc[e] = acc[e] + t;
-    }
-  }
-#pragma unroll
-  for (int e = 0; e < 8; ++e) dst[e] = acc[e];
-}
-
-// slot weights into LDS (one sc1 load per slot); ends with __syncthreads
-__device__ __forceinline__ void load_slot_weights(float* w, const void* topk_w) {
-  if (threadIdx.x < FX_SLOTS) w[threadIdx.x] = ldcf(topk_w, threadIdx.x);
-  __syncthreads();
 }
 
 // rmsnorm in place on xs (harness/numpy_ref.py:54-60): var = dot_lanes(x, x) / K,
@@ -167,23 +165,20 @@ __device__ __forceinline__ void rmsnorm_inplace(float* xs, const uint16_t* wn, i
   __syncthreads();
 }
 
-// greedy id from the per-worker (max, index) pairs: the lowest index among the maxima (one wave)
-__device__ __forceinline__ int64_t argmax_reduce(const void* amax, int nworkers) {
+// greedy id from the per-worker (max, index) packet pairs: the lowest index among the maxima (one
+// wave; result on every lane)
+__device__ __forceinline__ int64_t argmax_reduce(const void* amax, int nworkers, uint32_t tag, uint32_t* err) {
+  u32x4 v[4];
+  pk_wait_pairs<4>(amax, lane_id(), 64, nworkers, tag, err, v);
   float best = -__builtin_inff();
   int best_i = 0x7fffffff;
-  float v[4];
-  int id[4];
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
-    const int w = lane_id() + 64 * k;
-    const int ww = w < nworkers ? w : 0;
-    v[k] = ldcf(amax, 2 * ww);
-    id[k] = (int)ldc4(amax, (2 * ww + 1) * 4);
-    if (w >= nworkers) v[k] = -__builtin_inff();
+    if (lane_id() + 64 * k >= nworkers) continue;
+    const float fv = __uint_as_float(v[k].x);
+    const int id = (int)v[k].z;
+    if (fv > best || (fv == best && id < best_i)) { best = fv; best_i = id; }
   }
-#pragma unroll
-  for (int k = 0; k < 4; ++k)
-    if (v[k] > best || (v[k] == best && id[k] < best_i)) { best = v[k]; best_i = id[k]; }
   for (int off = 1; off < 64; off <<= 1) {
     float ov = shfl_xor_f(best, off);
     int oi = __shfl_xor(best_i, off, 64);
@@ -192,8 +187,33 @@ __device__ __forceinline__ int64_t argmax_reduce(const void* amax, int nworkers)
   return best_i;
 }
 
+// token of this iteration: tokens[step] inside the prompt, else the previous head's argmax (worker
+// 0 stores it to tokens[step]); kept in env.token. amax_tag: the previous head's output tag.
+__device__ __forceinline__ void embed_token(const void* amax, uint32_t amax_tag, FxEnv& env) {
+  int64_t* misc = (int64_t*)(env.lds + LDS_MISC);
+  if (wave_id() == 0) {
+    int64_t tok;
+    if (env.step < env.n_prompt) {
+      u32x2 t = ldc8(env.tokens, (uint32_t)env.step * 8);
+      tok = (int64_t)(((uint64_t)t.y << 32) | t.x);
+    } else {
+      tok = argmax_reduce(amax, env.nworkers, amax_tag, env.err);
+      if (env.worker == 0 && lane_id() == 0) {
+        u32x2 t;
+        t.x = (uint32_t)tok;
+        t.y = (uint32_t)((uint64_t)tok >> 32);
+        stc8(env.tokens, (uint32_t)env.step * 8, t);
+      }
+    }
+    if (lane_id() == 0) misc[0] = tok;
+  }
+  __syncthreads();
+  env.token = misc[0];
+  __syncthreads();
+}
+
 // ------------------------------------------------------------------------------------------------
-// FX_OP_GEMV
+// FX_OP_GEMV: rows in groups of 4, groups split over all workers
 
 template <int NJ>
 __device__ __forceinline__ void op_gemv_t(const fx_stage& s, FxEnv& env) {
@@ -203,55 +223,44 @@ __device__ __forceinline__ void op_gemv_t(const fx_stage& s, FxEnv& env) {
   float* rres = (float*)(env.lds + LDS_RES);
   const uint16_t* W = (const uint16_t*)s.w;
   const int K = s.k;
-  int r0, r1;
-  range_split(s.n_rows, env.nworkers, env.worker, r0, r1);
+  int g0, g1;
+  range_split((s.n_rows + 3) >> 2, env.nworkers, env.worker, g0, g1);
+  const int r0 = g0 * 4, r1 = g1 * 4 < s.n_rows ? g1 * 4 : s.n_rows;
   const int ngroups = (r1 - r0 + R - 1) / R;
   auto rowof = [&](int g, int i) { const int r = r0 + g * R + i; return r < r1 ? r : -1; };
   Tile<R, NJ> t0;
   gemv_prime(t0, W, K, ngroups, rowof);
+  const bool out_ll = (s.flags & FX_F_OUT_LL) != 0;
   const bool residual = (s.flags & FX_F_RESIDUAL) != 0;
-  if (residual)
-    for (int i = threadIdx.x; i < r1 - r0; i += FX_THREADS) rres[i] = bf2f(ldc2((const void*)s.res, (uint32_t)(r0 + i) * 2));
-  // ---- input row
+  const bool res_embed = (s.flags & FX_F_RES_EMBED) != 0;
+  // ---- token, input row, residual rows
   if (s.in_kind == FX_IN_EMBED) {
-    int64_t* misc = (int64_t*)(env.lds + LDS_MISC);
-    if (wave_id() == 0) {
-      int64_t tok;
-      if (env.step < env.n_prompt) {
-        u32x2 t = ldc8(env.tokens, (uint32_t)env.step * 8);
-        tok = (int64_t)(((uint64_t)t.y << 32) | t.x);
-      } else {
-        tok = argmax_reduce((const void*)s.aux[3], env.nworkers);
-        if (env.worker == 0 && lane_id() == 0) {
-          u32x2 t;
-          t.x = (uint32_t)tok;
-          t.y = (uint32_t)((uint64_t)tok >> 32);
-          stc8(env.tokens, (uint32_t)env.step * 8, t);
-        }
-      }
-      if (lane_id() == 0) misc[0] = tok;
-    }
-    __syncthreads();
-    const uint16_t* erow = (const uint16_t*)s.aux[0] + (size_t)misc[0] * K;
+    embed_token((const void*)s.aux[3], tag_in(s, env, 1), env);
+    const uint16_t* erow = (const uint16_t*)s.aux[0] + (size_t)env.token * K;
     for (int i = threadIdx.x * 8; i < K; i += FX_THREADS * 8) unpack8(ld16(erow + i), xs + i);
-  } else if (s.in_kind == FX_IN_COMBINE) {
-    float* w = (float*)(env.lds + LDS_MISC + 384);
-    load_slot_weights(w, (const void*)s.aux[1]);
-    for (int i = threadIdx.x * 8; i < K; i += FX_THREADS * 8) {
-      float a[8];
-      combine_chunk((const void*)s.x, (const void*)s.aux[0], w, K, i, a);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) xs[i + e] = bf16r(a[e]);
-    }
   } else {
-    load_vec_sc1(xs, (const void*)s.x, K);
+    poll_row(xs, (const void*)s.x, K, tag_in(s, env, 0), env.err);
   }
-  if ((s.flags & FX_F_WRITE_X) && env.worker == 0) store_vec_sc1((void*)s.aux[2], xs, K);
+  if (residual && threadIdx.x < ((r1 - r0 + 3) >> 2)) {
+    u32x4 v[1];
+    pk_wait_pairs<1>((const void*)s.res, (r0 >> 2) + threadIdx.x, 0, (r1 + 3) >> 2, tag_in(s, env, 2), env.err, v);
+    const int i = 4 * threadIdx.x;
+    rres[i + 0] = bf_lo(v[0].x);
+    rres[i + 1] = bf_hi(v[0].x);
+    rres[i + 2] = bf_lo(v[0].z);
+    rres[i + 3] = bf_hi(v[0].z);
+  }
+  if (res_embed) {
+    const uint16_t* erow = (const uint16_t*)s.aux[0] + (size_t)env.token * s.n_rows;
+    for (int i = threadIdx.x; i < r1 - r0; i += FX_THREADS) rres[i] = bf2f(erow[r0 + i]);
+  }
+  prof_mark(env, 1);
   if (s.flags & FX_F_NORM) rmsnorm_inplace(xs, (const uint16_t*)s.w_norm, K, s.eps, red);
   else __syncthreads();
   // ---- rows
   void* out = (void*)s.out;
   const bool want_max = (s.flags & FX_F_ARGMAX) != 0;
+  const bool add_res = residual || res_embed;
   float best = -__builtin_inff();
   int best_i = 0x7fffffff;
   gemv_pipe(t0, W, K, xs, ngroups, rowof, [&](int g, const int* row, const float* acc) {
@@ -260,15 +269,26 @@ __device__ __forceinline__ void op_gemv_t(const fx_stage& s, FxEnv& env) {
     for (int i = 0; i < R; ++i) {
       if (row[i] < 0) continue;
       float v = acc[i];
-      if (residual) v = v + rres[row[i] - r0];
+      if (add_res) v = v + rres[row[i] - r0];
       const uint32_t b = f2bf(v);
-      if (lane == i) stc2(out, (uint32_t)row[i] * 2, b);
+      if (out_ll) {
+        if (lane == 0) rres[FX_MAX_OUT_ROWS / 2 + row[i] - r0] = bf2f(b);
+      } else if (lane == i) {
+        stc2(out, (uint32_t)row[i] * 2, b);
+      }
       if (want_max) {
         const float fv = bf2f(b);
         if (fv > best || (fv == best && row[i] < best_i)) { best = fv; best_i = row[i]; }
       }
     }
   });
+  if (out_ll) {
+    __syncthreads();
+    const float* o = rres + FX_MAX_OUT_ROWS / 2;
+    const uint32_t tag = tag_out(env);
+    for (int t = threadIdx.x; 4 * t < r1 - r0; t += FX_THREADS)
+      pk_put2(out, (uint32_t)((r0 >> 1) + 2 * t), pack2(o[4 * t], o[4 * t + 1]), pack2(o[4 * t + 2], o[4 * t + 3]), tag);
+  }
   if (want_max) {
     float* rv = red + 16;
     int* ri = (int*)(red + 32);
@@ -279,10 +299,10 @@ __device__ __forceinline__ void op_gemv_t(const fx_stage& s, FxEnv& env) {
       int bi = ri[0];
       for (int w = 1; w < FX_WAVES; ++w)
         if (rv[w] > b || (rv[w] == b && ri[w] < bi)) { b = rv[w]; bi = ri[w]; }
-      stcf((void*)s.aux[3], 2 * env.worker, b);
-      stc4((void*)s.aux[3], (2 * env.worker + 1) * 4, (uint32_t)bi);
+      pk_put2((void*)s.aux[3], (uint32_t)(2 * env.worker), __float_as_uint(b), (uint32_t)bi, tag_out(env));
     }
   }
+  prof_mark(env, 2);
 }
 
 __device__ __forceinline__ void op_gemv(const fx_stage& s, FxEnv& env) {
@@ -296,7 +316,7 @@ __device__ __forceinline__ void op_gemv(const fx_stage& s, FxEnv& env) {
 // ------------------------------------------------------------------------------------------------
 // gate|up pairs with SiLU (harness/numpy_ref.py:256-292 fused): act[i] = bf16(silu(g) * u),
 // g = bf16(W[i] h), u = bf16(W[I + i] h). Pairs [p0, p1) of the I pairs of W (2I rows); a group
-// is 2 pairs = rows (p, I + p, p + 1, I + p + 1).
+// is 2 pairs = rows (p, I + p, p + 1, I + p + 1), whose two act values form one packet.
 
 struct PairRows {
   int p0, p1, I;
@@ -307,16 +327,18 @@ struct PairRows {
   }
 };
 
-__device__ __forceinline__ void gate_up_emit(void* act, uint32_t act_off, const int* row, const float* acc) {
-  const int lane = lane_id();
+// act packet of the group (pairs row[0], row[2]) at packet index pkt_base + row[0] / 2
+__device__ __forceinline__ void gate_up_emit(void* act, uint32_t pkt_base, const int* row, const float* acc,
+                                             uint32_t tag) {
+  float a[2] = {0.0f, 0.0f};
 #pragma unroll
   for (int q = 0; q < 2; ++q) {
     if (row[2 * q] < 0) continue;
     const float gv = bf16r(acc[2 * q]);
     const float uv = bf16r(acc[2 * q + 1]);
-    const float a = silu_s(gv) * uv;
-    if (lane == q) stc2(act, act_off + (uint32_t)row[2 * q] * 2, f2bf(a));
+    a[q] = silu_s(gv) * uv;
   }
+  if (lane_id() == 0 && row[0] >= 0) pk_put(act, pkt_base + (uint32_t)(row[0] >> 1), pack2(a[0], a[1]), tag);
 }
 
 // FX_OP_DENSE_GU: layer-0 gate/up + SiLU over all workers (HF DeepseekV2MLP,
@@ -327,14 +349,20 @@ __device__ __forceinline__ void op_dense_gu(const fx_stage& s, FxEnv& env) {
   const int K = s.k, I = s.n_rows;
   const uint16_t* W = (const uint16_t*)s.w;
   PairRows rowof;
-  range_split(I, env.nworkers, env.worker, rowof.p0, rowof.p1);
+  int q0, q1;
+  range_split(I >> 1, env.nworkers, env.worker, q0, q1);
+  rowof.p0 = 2 * q0;
+  rowof.p1 = 2 * q1;
   rowof.I = I;
-  const int ngroups = (rowof.p1 - rowof.p0 + 1) / 2;
+  const int ngroups = q1 - q0;
   Tile<4, 4> t0;
   gemv_prime(t0, W, K, ngroups, rowof);
-  load_vec_sc1(xs, (const void*)s.x, K);
+  poll_row(xs, (const void*)s.x, K, tag_in(s, env, 0), env.err);
+  prof_mark(env, 1);
   rmsnorm_inplace(xs, (const uint16_t*)s.w_norm, K, s.eps, red);
   if (s.aux[6] && env.worker == 0) store_vec_sc1((void*)s.aux[6], xs, K);
   void* act = (void*)s.out;
-  gemv_pipe(t0, W, K, xs, ngroups, rowof, [&](int g, const int* row, const float* acc) { gate_up_emit(act, 0, row, acc); });
+  const uint32_t tag = tag_out(env);
+  gemv_pipe(t0, W, K, xs, ngroups, rowof, [&](int g, const int* row, const float* acc) { gate_up_emit(act, 0, row, acc, tag); });
+  prof_mark(env, 2);
 }

@@ -1,9 +1,13 @@
-// MoE operators: router, expert gate|up + SiLU, expert down, combine; the argmax reduce.
-// harness/numpy_ref.py:205-292, 316-321; the reference's moe_router_mi300.cuh:115-354,
+// MoE operators: router, expert gate|up + SiLU, expert down fused with the combine; the argmax
+// reduce. harness/numpy_ref.py:205-292, 316-321; the reference's moe_router_mi300.cuh:115-354,
 // gang_moe_w13_gemv_mi300.cuh:101-219, gang_moe_w2_silu_mi300.cuh and moe_mul_sum_add.
-// Slot s of the 8 (top-6 routed, then the two shared experts E, E+1 at weight 1.0) runs on XCD s.
+// Slot s of the 8 (top-6 routed, then the two shared experts E, E+1 at weight 1.0): its gate|up
+// runs on XCD s; its down projection is spread over every worker (8 output rows each, all slots),
+// so the combine of a row happens where its eight slot values are.
 #pragma once
 #include "fx_gemv.h"
+
+#define FX_SLOTS 8
 
 // Router softmax + top-k on one wave: lane e holds logit e; the softmax sum is the xor butterfly
 // over pow2ceil(E) lanes; top-k by repeated argmax, lowest index on ties (numpy_ref.py:216-227).
@@ -30,30 +34,52 @@ __device__ __forceinline__ void softmax_topk_wave(const float* logits, int E, in
   }
 }
 
-// FX_OP_MOE_ROUTER: per XCD, h = rmsnorm(x_res), logits rows e = rank, rank + 31, ... of the XCD's
-// workers into logits_x[xcd] (each routed XCD computes its own copy).
-__device__ __forceinline__ void op_moe_router(const fx_stage& s, FxEnv& env) {
-  if (env.xcd >= s.topk) return;   // forced-expert slots need no routing
-  float* xs = (float*)(env.lds + LDS_XS);
-  float* red = (float*)(env.lds + LDS_RED);
-  const int K = s.k, E = s.n_rows;
-  const uint16_t* W = (const uint16_t*)s.w;
-  const int per = (E + env.xworkers - 1) / env.xworkers;
-  auto rowof = [&](int g, int i) { const int r = env.xrank + i * env.xworkers; return (i < per && r < E) ? r : -1; };
-  Tile<4, 4> t0;
-  gemv_prime(t0, W, K, 1, rowof);
-  load_vec_sc1(xs, (const void*)s.x, K);
-  rmsnorm_inplace(xs, (const uint16_t*)s.w_norm, K, s.eps, red);
-  void* lx = (void*)s.out;
-  gemv_pipe(t0, W, K, xs, 1, rowof, [&](int g, const int* row, const float* acc) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      if (row[i] >= 0 && lane_id() == i) stcf(lx, env.xcd * E + row[i], acc[i]);
-  });
+// wave 0: the E router logits (packets, f32) into lg[0, E)
+__device__ __forceinline__ void poll_logits_wave(float* lg, const void* src, int E, uint32_t tag, uint32_t* err) {
+  u32x4 v[1];
+  pk_wait_pairs<1>(src, lane_id(), 0, E >> 1, tag, err, v);
+  if (2 * lane_id() < E) {
+    lg[2 * lane_id()] = __uint_as_float(v[0].x);
+    lg[2 * lane_id() + 1] = __uint_as_float(v[0].z);
+  }
 }
 
-// FX_OP_MOE_W13: per XCD, slot = XCD; the slot's expert from the XCD's router logits, then
-// act8[slot][i] = bf16(silu(bf16(W13[e][i] h)) * bf16(W13[e][I + i] h)) over the XCD's workers.
+// expert of each slot and its combine weight: ids/wts (LDS, n_slots entries) from the E logits
+// (wave 0; the caller syncs)
+__device__ __forceinline__ void route_slots_wave(const float* lg, const fx_stage& s, int* ids, float* wts, float* probs) {
+  const int E = s.aux_i0 > 0 ? s.aux_i0 : s.n_rows;
+  softmax_topk_wave(lg, E, s.topk, s.scaling, ids, wts, probs);
+  if (lane_id() < s.n_forced) {
+    ids[s.topk + lane_id()] = E + lane_id();
+    wts[s.topk + lane_id()] = 1.0f;
+  }
+}
+
+// FX_OP_MOE_ROUTER: h = rmsnorm(x_res), logits[e] = dot_lanes(W_gate[e], h) on worker e.
+__device__ __forceinline__ void op_moe_router(const fx_stage& s, FxEnv& env) {
+  const int E = s.n_rows;
+  if (env.worker >= E) return;
+  float* xs = (float*)(env.lds + LDS_XS);
+  float* red = (float*)(env.lds + LDS_RED);
+  const int K = s.k;
+  const uint16_t* W = (const uint16_t*)s.w;
+  const int e = env.worker;
+  auto rowof = [&](int g, int i) { return e; };
+  Tile<1, 4> t0;
+  gemv_prime(t0, W, K, 1, rowof);
+  poll_row(xs, (const void*)s.x, K, tag_in(s, env, 0), env.err);
+  prof_mark(env, 1);
+  rmsnorm_inplace(xs, (const uint16_t*)s.w_norm, K, s.eps, red);
+  const uint32_t tag = tag_out(env);
+  gemv_pipe(t0, W, K, xs, 1, rowof, [&](int g, const int* row, const float* acc) {
+    if (lane_id() == 0) pk_put((void*)s.out, (uint32_t)e, __float_as_uint(acc[0]), tag);
+  });
+  prof_mark(env, 2);
+}
+
+// FX_OP_MOE_W13: slot = XCD; the slot's expert from the router logits (routed slots) or fixed
+// (shared slots), then act8[slot][i] = bf16(silu(bf16(W13[e][i] h)) * bf16(W13[e][I + i] h)) over
+// the XCD's 32 workers. A shared slot issues its weight loads before anything arrives.
 __device__ __forceinline__ void op_moe_w13(const fx_stage& s, FxEnv& env) {
   float* xs = (float*)(env.lds + LDS_XS);
   float* red = (float*)(env.lds + LDS_RED);
@@ -64,18 +90,30 @@ __device__ __forceinline__ void op_moe_w13(const fx_stage& s, FxEnv& env) {
   const int slot = env.xcd;
   const int topk = s.topk;
   const bool routed = slot < topk;
-  const bool writer = env.xcd == 0 && env.xrank == 0;
+  const bool writer = env.worker == 0;
   float* lg = red + 256;
-  // the input row and this XCD's logits are independent loads: issue both first
-  if (routed || writer)
-    for (int i = threadIdx.x; i < E; i += FX_THREADS) lg[i] = ldcf((const void*)s.aux[0], env.xcd * E + i);
-  load_vec_sc1(xs, (const void*)s.x, K);
+  PairRows rowof;
+  int q0, q1;
+  range_split(I >> 1, env.xworkers, env.xrank, q0, q1);
+  rowof.p0 = 2 * q0;
+  rowof.p1 = 2 * q1;
+  rowof.I = I;
+  const int ngroups = q1 - q0;
+  Tile<4, 4> t0;
+  const uint16_t* W = nullptr;
+  if (!routed) {
+    W = (const uint16_t*)s.w + (size_t)(E + slot - topk) * 2 * I * K;
+    gemv_prime(t0, W, K, ngroups, rowof);
+  }
+  if ((routed || writer) && wave_id() == 0) poll_logits_wave(lg, (const void*)s.aux[0], E, tag_in(s, env, 0), env.err);
+  poll_row(xs, (const void*)s.x, K, tag_in(s, env, 1), env.err);
+  prof_mark(env, 1);
   __syncthreads();
   if (wave_id() == 0) {
     int e = E + (slot - topk);
     if (routed || writer) {
       float* probs = red + 512;
-      softmax_topk_wave(lg, E, topk, s.scaling, ids, wts, probs);
+      route_slots_wave(lg, s, ids, wts, probs);
       if (routed) e = ids[slot];
       if (writer) {
         // router outputs in numpy_ref.moe_router's layout: topk_w, routing, mask, logits, route_log
@@ -83,24 +121,21 @@ __device__ __forceinline__ void op_moe_w13(const fx_stage& s, FxEnv& env) {
         const int lane = lane_id();
         const int row = env.step - (env.n_prompt - 1);
         for (int k = lane; k < n_slots; k += 64) {
-          const int id = k < topk ? ids[k] : E + (k - topk);
-          stcf((void*)s.aux[1], k, k < topk ? wts[k] : 1.0f);
+          stcf((void*)s.aux[1], k, wts[k]);
           // route_log [prow][aux_i1][n_slots] at row step - (n_prompt - 1): the decode iterations,
           // as the reference logs them (route_log [32, 26, 8] at [step - 1023])
           if (s.aux[5] && s.layer >= 1 && row >= 0 && row < s.prow)
-            stc4((void*)s.aux[5], (uint32_t)(((row * s.aux_i1) + (s.layer - 1)) * n_slots + k) * 4, (uint32_t)id);
+            stc4((void*)s.aux[5], (uint32_t)(((row * s.aux_i1) + (s.layer - 1)) * n_slots + k) * 4, (uint32_t)ids[k]);
         }
         for (int x = lane; x < n_total; x += 64) {
           int r = 0;
-          for (int k = 0; k < n_slots; ++k) {
-            const int id = k < topk ? ids[k] : E + (k - topk);
-            if (id == x) r = k + 1;
-          }
+          for (int k = 0; k < n_slots; ++k)
+            if (ids[k] == x) r = k + 1;
           stc4((void*)s.aux[2], x * 4, (uint32_t)r);
         }
         for (int x = lane; x <= n_total; x += 64) {
           int v = -1;
-          if (x < n_slots) v = x < topk ? ids[x] : E + (x - topk);
+          if (x < n_slots) v = ids[x];
           if (x == n_total) v = n_slots;
           stc4((void*)s.aux[3], x * 4, (uint32_t)v);
         }
@@ -108,80 +143,106 @@ __device__ __forceinline__ void op_moe_w13(const fx_stage& s, FxEnv& env) {
       }
     }
     if (lane_id() == 0) misc[0] = e;
-    if (env.xrank == 0 && lane_id() == 0) stc4((void*)s.aux[7], slot * 4, (uint32_t)e);
+    if (env.xrank == 0 && lane_id() == 0 && s.aux[7]) stc4((void*)s.aux[7], slot * 4, (uint32_t)e);
   }
   __syncthreads();
-  const int e = misc[0];
-  env.moe_e = e;
-  const uint16_t* W = (const uint16_t*)s.w + (size_t)e * 2 * I * K;
-  PairRows rowof;
-  range_split(I, env.xworkers, env.xrank, rowof.p0, rowof.p1);
-  rowof.I = I;
-  const int ngroups = (rowof.p1 - rowof.p0 + 1) / 2;
-  Tile<4, 4> t0;
-  gemv_prime(t0, W, K, ngroups, rowof);
+  if (routed) {
+    W = (const uint16_t*)s.w + (size_t)misc[0] * 2 * I * K;
+    gemv_prime(t0, W, K, ngroups, rowof);
+  }
   rmsnorm_inplace(xs, (const uint16_t*)s.w_norm, K, s.eps, red);
   if (s.aux[6] && writer) store_vec_sc1((void*)s.aux[6], xs, K);
   void* act = (void*)s.out;
-  const uint32_t off = (uint32_t)slot * I * 2;
-  gemv_pipe(t0, W, K, xs, ngroups, rowof, [&](int g, const int* row, const float* acc) { gate_up_emit(act, off, row, acc); });
+  const uint32_t base = (uint32_t)slot * (I >> 1);
+  const uint32_t tag = tag_out(env);
+  gemv_pipe(t0, W, K, xs, ngroups, rowof, [&](int g, const int* row, const float* acc) { gate_up_emit(act, base, row, acc, tag); });
+  prof_mark(env, 2);
 }
 
-// FX_OP_MOE_W2: per XCD, out8[slot] = bf16(W2[e] act8[slot]). Inside the persistent kernel the
-// expert is the one this workgroup's W13 stage chose; a standalone launch reads it from sel.
+// FX_OP_MOE_W2 with the combine: worker w owns output rows [r0, r0 + 8) of every slot; group g is
+// 4 rows of one slot (shared slots first, so their loads go out before the logits arrive);
+// x_new[n] = bf16(x[n] + sum_s out8[s][n] * w_s), multiply then add, in slot order
+// (harness/numpy_ref.py:316-321).
+#define W2_ROWS 8
 __device__ __forceinline__ void op_moe_w2(const fx_stage& s, FxEnv& env) {
-  float* xs = (float*)(env.lds + LDS_XS);
-  int* misc = (int*)(env.lds + LDS_MISC);
+  float* xs = (float*)(env.lds + LDS_XS);        // act8 [8][I]
+  float* red = (float*)(env.lds + LDS_RED);
+  int* ids = (int*)(env.lds + LDS_MISC + 128);
+  float* wts = (float*)(env.lds + LDS_MISC + 256);
+  float* rres = (float*)(env.lds + LDS_RES);     // x rows [8], then out8 [8 slots][8 rows] at +16
   const int I = s.k, H = s.n_rows;
-  const int slot = env.xcd;
-  int e = env.moe_e;
-  if (e < 0) {
-    if (threadIdx.x == 0) misc[0] = (int)ldc4((const void*)s.aux[7], slot * 4);
-    __syncthreads();
-    e = misc[0];
-  }
-  const uint16_t* W = (const uint16_t*)s.w + (size_t)e * H * I;
-  int r0, r1;
-  range_split(H, env.xworkers, env.xrank, r0, r1);
-  const int ngroups = (r1 - r0 + 3) / 4;
-  auto rowof = [&](int g, int i) { const int r = r0 + g * 4 + i; return r < r1 ? r : -1; };
-  Tile<4, 3> t0;
-  gemv_prime(t0, W, I, ngroups, rowof);
-  load_vec_sc1(xs, (const uint8_t*)s.x + (size_t)slot * I * 2, I);
-  __syncthreads();
-  void* out = (void*)s.out;
-  gemv_pipe(t0, W, I, xs, ngroups, rowof, [&](int g, const int* row, const float* acc) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      if (row[i] >= 0 && lane_id() == i) stc2(out, (uint32_t)(slot * H + row[i]) * 2, f2bf(acc[i]));
-  });
-}
-
-// FX_OP_MOE_COMBINE (standalone form; inside the decode it is the next GEMV's input prologue)
-__device__ __forceinline__ void op_moe_combine(const fx_stage& s, FxEnv& env) {
-  const int H = s.n_rows;
+  const int nslots = FX_SLOTS;
+  const int nsh = s.n_forced;
+  const int E = s.aux_i0;
   int c0, c1;
-  range_split(H / 8, env.nworkers, env.worker, c0, c1);
-  float* w = (float*)(env.lds + LDS_MISC + 384);
-  load_slot_weights(w, (const void*)s.aux[1]);
-  for (int c = c0 + (int)threadIdx.x; c < c1; c += FX_THREADS) {
-    const int i = c * 8;
-    float a[8];
-    combine_chunk((const void*)s.x, (const void*)s.aux[0], w, H, i, a);
-    u32x4 r;
-    r.x = pack2(a[0], a[1]);
-    r.y = pack2(a[2], a[3]);
-    r.z = pack2(a[4], a[5]);
-    r.w = pack2(a[6], a[7]);
-    stc16((void*)s.out, (uint32_t)i * 2, r);
+  range_split(H / W2_ROWS, env.nworkers, env.worker, c0, c1);
+  const int r0 = c0 * W2_ROWS;
+  const int nrow = (c1 - c0) * W2_ROWS;          // 8 (H = 2048, 256 workers)
+  const int quads = nrow >> 2;
+  const int ngroups = nslots * quads;
+  // group g -> slot (shared first), quad
+  auto slot_of = [&](int g) { const int k = g / quads; return k < nsh ? s.topk + k : k - nsh; };
+  auto rowof = [&](int g, int i) {
+    const int sl = slot_of(g);
+    const int e = sl < s.topk ? ids[sl] : E + (sl - s.topk);
+    return e * H + r0 + (g % quads) * 4 + i;
+  };
+  const uint16_t* W = (const uint16_t*)s.w;
+  Tile<4, 3> t0;
+  // shared-slot groups first: wave v's first group is v, a shared slot when v < nsh * quads
+  if (wave_id() < nsh * quads) tile_load(t0, W, I, wave_id(), rowof);
+  if (wave_id() == 0) {
+    float* lg = red + 256;
+    poll_logits_wave(lg, (const void*)s.aux[0], E, tag_in(s, env, 1), env.err);
+    route_slots_wave(lg, s, ids, wts, nullptr);
   }
+  if (threadIdx.x < (nrow >> 2)) {
+    u32x4 v[1];
+    pk_wait_pairs<1>((const void*)s.res, (r0 >> 2) + threadIdx.x, 0, (r0 + nrow) >> 2, tag_in(s, env, 2), env.err, v);
+    const int i = 4 * threadIdx.x;
+    rres[i + 0] = bf_lo(v[0].x);
+    rres[i + 1] = bf_hi(v[0].x);
+    rres[i + 2] = bf_lo(v[0].z);
+    rres[i + 3] = bf_hi(v[0].z);
+  }
+  __syncthreads();
+  if (wave_id() >= nsh * quads && wave_id() < ngroups) tile_load(t0, W, I, wave_id(), rowof);
+  poll_row(xs, (const void*)s.x, nslots * I, tag_in(s, env, 0), env.err);
+  prof_mark(env, 1);
+  __syncthreads();
+  float* o8 = rres + 16;
+  gemv_pipe_x(t0, W, I, [&](int g) { return (const float*)(xs + slot_of(g) * I); }, ngroups, rowof,
+              [&](int g, const int* row, const float* acc) {
+                if (lane_id() == 0) {
+                  const int sl = slot_of(g);
+#pragma unroll
+                  for (int i = 0; i < 4; ++i) o8[sl * W2_ROWS + (g % quads) * 4 + i] = bf16r(acc[i]);
+                }
+              });
+  __syncthreads();
+  if (threadIdx.x < nrow) {
+    const int r = threadIdx.x;
+    float acc = rres[r];
+    for (int sl = 0; sl < nslots; ++sl) {
+      const float t = o8[sl * W2_ROWS + r] * wts[sl];
+      acc = acc + t;
+    }
+    red[r] = bf16r(acc);
+    if (s.aux[1])
+      for (int sl = 0; sl < nslots; ++sl) stc2((void*)s.aux[1], (uint32_t)(sl * H + r0 + r) * 2, f2bf(o8[sl * W2_ROWS + r]));
+  }
+  __syncthreads();
+  if (threadIdx.x < (nrow >> 1))
+    pk_put((void*)s.out, (uint32_t)((r0 >> 1) + threadIdx.x), pack2(red[2 * threadIdx.x], red[2 * threadIdx.x + 1]),
+           tag_out(env));
+  prof_mark(env, 2);
 }
 
 // FX_OP_ARGMAX: tokens[step + 1] (the reduce of argmax_partial; fleet/graph_plan.py:598-602)
 __device__ __forceinline__ void op_argmax(const fx_stage& s, FxEnv& env) {
   if (env.worker != 0 || wave_id() != 0) return;
   if (env.step + 1 < env.n_prompt) return;
-  const int64_t tok = argmax_reduce((const void*)s.aux[3], env.nworkers);
+  const int64_t tok = argmax_reduce((const void*)s.aux[3], env.nworkers, tag_in(s, env, 0), env.err);
   if (lane_id() == 0) {
     u32x2 t;
     t.x = (uint32_t)tok;

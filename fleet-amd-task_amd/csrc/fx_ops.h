@@ -2,8 +2,8 @@
 // worker workgroup (256 threads) for its share of the stage. The same code runs inside the
 // persistent kernel and in the per-stage launcher of the kernel suite.
 //   fx_gemv.h  GEMV (qkva, o_proj, dense down, LM head + argmax), dense gate|up + SiLU
-//   fx_moe.h   router, expert gate|up + SiLU, expert down, combine, argmax reduce
-//   fx_mla.h   MLA prep (norm, RoPE, cache append, W_uk absorb), split-KV attend + LSE merge, W_uv
+//   fx_moe.h   router, expert gate|up + SiLU, expert down + combine, argmax reduce
+//   fx_mla.h   MLA prep (norm, RoPE, cache append, W_uk absorb), split-KV attend, LSE merge + W_uv
 #pragma once
 #include "fx_mla.h"
 #include "fx_moe.h"
@@ -17,7 +17,6 @@ __device__ __forceinline__ void run_stage(const fx_stage& s, FxEnv& env) {
     case FX_OP_MOE_ROUTER: op_moe_router(s, env); break;
     case FX_OP_MOE_W13: op_moe_w13(s, env); break;
     case FX_OP_MOE_W2: op_moe_w2(s, env); break;
-    case FX_OP_MOE_COMBINE: op_moe_combine(s, env); break;
     case FX_OP_DENSE_GU: op_dense_gu(s, env); break;
     case FX_OP_ARGMAX: op_argmax(s, env); break;
     default: break;

@@ -1,0 +1,206 @@
+// Hardware probes of the gfx950 memory system that the decode kernel's design rests on
+// (the reference's env/hw/probes/stream_read.cu, chase.cu and fence_probe.cu, re-written for
+// MI355X): the HBM stream rate of the GEMV load pattern as a function of bytes per workgroup and
+// loads in flight, the latency of one dependent load per cache policy (idle and under a streaming
+// load), and the round trip of a flag between two workgroups on the same or different XCDs.
+// Every loop is bounded; nothing here waits on a condition without a tick limit.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "fx_device.h"
+
+#define PROBE_LIMIT (100ull * 1000 * 1000)   // 1 s of s_memrealtime ticks: every wait gives up after it
+
+typedef uint32_t u32x4p __attribute__((ext_vector_type(4)));
+
+// ---- stream: block b reads [b * bytes, (b + 1) * bytes) of src with the GEMV pattern: each wave
+// issues `depth` 1 KiB loads (64 lanes x 16 B) before consuming them; stamps per block.
+template <int D>
+__device__ void stream_body(const uint8_t* src, uint64_t bytes, uint64_t* ticks, uint32_t* sink) {
+  const uint8_t* base = src + (uint64_t)blockIdx.x * bytes;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+  uint32_t acc = 0;
+  const uint64_t step = (uint64_t)nw * D * 1024;
+  for (uint64_t off = (uint64_t)wave * D * 1024; off < bytes; off += step) {
+    u32x4p v[D];
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      uint64_t o = off + (uint64_t)d * 1024 + lane * 16;
+      if (o + 16 > bytes) o = lane * 16;
+      v[d] = __builtin_nontemporal_load((const u32x4p*)(base + o));
+    }
+#pragma unroll
+    for (int d = 0; d < D; ++d) acc += v[d].x ^ v[d].y ^ v[d].z ^ v[d].w;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) ticks[blockIdx.x] = __builtin_amdgcn_s_memrealtime() - t0;
+  if (acc == 0x12345678u) sink[0] = acc;
+}
+
+__global__ void fxp_stream_kernel(const uint8_t* src, uint64_t bytes, int depth, uint64_t* ticks, uint32_t* sink) {
+  switch (depth) {
+    case 4: stream_body<4>(src, bytes, ticks, sink); break;
+    case 8: stream_body<8>(src, bytes, ticks, sink); break;
+    case 16: stream_body<16>(src, bytes, ticks, sink); break;
+    default: stream_body<32>(src, bytes, ticks, sink); break;
+  }
+}
+
+// ---- chase: block 0 lane 0 follows idx[] for `hops` dependent loads with the chosen policy;
+// blocks 1.. stream-read `load` (if non-null) until block 0 is done or a tick limit passes.
+__device__ __forceinline__ uint32_t ld_policy(const uint32_t* p, uint32_t i, int mode) {
+  if (mode == 1) return __builtin_amdgcn_raw_buffer_load_b32(rsrc(p), i * 4, 0, FX_SC1);
+  if (mode == 2) return __builtin_nontemporal_load(p + i);
+  return __hip_atomic_load(const_cast<uint32_t*>(p + i), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
+}
+
+__global__ void fxp_chase_kernel(const uint32_t* idx, uint32_t hops, int mode, const uint8_t* load, uint64_t load_bytes,
+                                 uint32_t* done, uint64_t* out) {
+  if (blockIdx.x == 0) {
+    if (threadIdx.x == 0) {
+      uint32_t j = 0;
+      // warm the first access (TLB), then time
+      j = ld_policy(idx, j, mode);
+      const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+      for (uint32_t h = 0; h < hops; ++h) j = ld_policy(idx, j, mode);
+      const uint64_t t1 = __builtin_amdgcn_s_memrealtime();
+      out[0] = t1 - t0;
+      out[1] = j;
+      __hip_atomic_store(done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    return;
+  }
+  if (!load) return;
+  const uint64_t per = load_bytes / gridDim.x;
+  const uint8_t* base = load + (uint64_t)blockIdx.x * per;
+  const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+  uint32_t acc = 0;
+  for (int rep = 0; rep < 1000; ++rep) {
+    for (uint64_t off = threadIdx.x * 16; off + 16 * 8 * blockDim.x <= per; off += 16 * 8 * blockDim.x) {
+      u32x4p v[8];
+#pragma unroll
+      for (int d = 0; d < 8; ++d) v[d] = __builtin_nontemporal_load((const u32x4p*)(base + off + (uint64_t)d * 16 * blockDim.x));
+#pragma unroll
+      for (int d = 0; d < 8; ++d) acc += v[d].x;
+    }
+    if (__hip_atomic_load(done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ||
+        __builtin_amdgcn_s_memrealtime() - t0 > PROBE_LIMIT)
+      break;
+  }
+  if (acc == 0x12345678u) out[2] = acc;
+}
+
+// ---- ping-pong between block a and block b (cooperative launch of `grid` blocks): a stores
+// flag[0] = i, b waits for it and stores flag[32] = i, a waits; `rounds` round trips, stamped by a.
+// Other blocks stream-read `load` while the exchange runs (if non-null).
+__global__ void fxp_pingpong_kernel(uint32_t* flag, int a, int b, uint32_t rounds, const uint8_t* load, uint64_t load_bytes,
+                                    uint64_t* out) {
+  const int blk = blockIdx.x;
+  if (blk == a || blk == b) {
+    if (threadIdx.x != 0) return;
+    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+    bool ok = true;
+    for (uint32_t i = 1; i <= rounds && ok; ++i) {
+      if (blk == a) {
+        __hip_atomic_store(&flag[0], i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        while (__hip_atomic_load(&flag[32], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != i)
+          if (__builtin_amdgcn_s_memrealtime() - t0 > PROBE_LIMIT) { ok = false; break; }
+      } else {
+        while (__hip_atomic_load(&flag[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != i)
+          if (__builtin_amdgcn_s_memrealtime() - t0 > PROBE_LIMIT) { ok = false; break; }
+        __hip_atomic_store(&flag[32], i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+    if (blk == a) {
+      out[0] = __builtin_amdgcn_s_memrealtime() - t0;
+      out[1] = ok ? 1 : 0;
+      __hip_atomic_store(&flag[64], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    return;
+  }
+  if (!load) return;
+  const uint64_t per = load_bytes / gridDim.x;
+  const uint8_t* base = load + (uint64_t)blk * per;
+  const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+  uint32_t acc = 0;
+  for (int rep = 0; rep < 1000; ++rep) {
+    for (uint64_t off = threadIdx.x * 16; off + 16 * 8 * blockDim.x <= per; off += 16 * 8 * blockDim.x) {
+      u32x4p v[8];
+#pragma unroll
+      for (int d = 0; d < 8; ++d) v[d] = __builtin_nontemporal_load((const u32x4p*)(base + off + (uint64_t)d * 16 * blockDim.x));
+#pragma unroll
+      for (int d = 0; d < 8; ++d) acc += v[d].x;
+    }
+    if (__hip_atomic_load(&flag[64], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ||
+        __builtin_amdgcn_s_memrealtime() - t0 > PROBE_LIMIT)
+      break;
+  }
+  if (acc == 0x12345678u) out[2] = acc;
+}
+
+extern "C" {
+
+// all functions: 0 on success, else the hipError_t value
+int fxp_stream(const void* src, uint64_t bytes_per_block, int blocks, int threads, int depth, uint64_t* ticks_host,
+               float* ms) {
+  uint64_t* d_ticks = nullptr;
+  uint32_t* sink = nullptr;
+  hipEvent_t e0, e1;
+  hipError_t e;
+  if ((e = hipMalloc(&d_ticks, 8 * blocks)) != hipSuccess) return e;
+  if ((e = hipMalloc(&sink, 64)) != hipSuccess) return e;
+  (void)hipEventCreate(&e0);
+  (void)hipEventCreate(&e1);
+  (void)hipEventRecord(e0, 0);
+  hipLaunchKernelGGL(fxp_stream_kernel, dim3(blocks), dim3(threads), 0, 0, (const uint8_t*)src, bytes_per_block, depth,
+                     d_ticks, sink);
+  (void)hipEventRecord(e1, 0);
+  if ((e = hipEventSynchronize(e1)) != hipSuccess) return e;
+  (void)hipEventElapsedTime(ms, e0, e1);
+  e = hipMemcpy(ticks_host, d_ticks, 8 * blocks, hipMemcpyDeviceToHost);
+  (void)hipFree(d_ticks);
+  (void)hipFree(sink);
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  return e;
+}
+
+int fxp_chase(const uint32_t* idx, uint32_t hops, int mode, const void* load, uint64_t load_bytes, int blocks,
+              uint64_t* out_host) {
+  uint32_t* done = nullptr;
+  uint64_t* out = nullptr;
+  hipError_t e;
+  if ((e = hipMalloc(&done, 256)) != hipSuccess) return e;
+  if ((e = hipMalloc(&out, 64)) != hipSuccess) return e;
+  (void)hipMemset(done, 0, 256);
+  (void)hipMemset(out, 0, 64);
+  void* args[] = {(void*)&idx, &hops, &mode, (void*)&load, &load_bytes, &done, &out};
+  if ((e = hipLaunchCooperativeKernel((const void*)fxp_chase_kernel, dim3(blocks), dim3(256), args, 0, 0)) != hipSuccess)
+    return e;
+  if ((e = hipDeviceSynchronize()) != hipSuccess) return e;
+  e = hipMemcpy(out_host, out, 24, hipMemcpyDeviceToHost);
+  (void)hipFree(done);
+  (void)hipFree(out);
+  return e;
+}
+
+int fxp_pingpong(int a, int b, uint32_t rounds, const void* load, uint64_t load_bytes, int blocks, uint64_t* out_host) {
+  uint32_t* flag = nullptr;
+  uint64_t* out = nullptr;
+  hipError_t e;
+  if ((e = hipMalloc(&flag, 1024)) != hipSuccess) return e;
+  if ((e = hipMalloc(&out, 64)) != hipSuccess) return e;
+  (void)hipMemset(flag, 0, 1024);
+  (void)hipMemset(out, 0, 64);
+  void* args[] = {&flag, &a, &b, &rounds, (void*)&load, &load_bytes, &out};
+  if ((e = hipLaunchCooperativeKernel((const void*)fxp_pingpong_kernel, dim3(blocks), dim3(256), args, 0, 0)) != hipSuccess)
+    return e;
+  if ((e = hipDeviceSynchronize()) != hipSuccess) return e;
+  e = hipMemcpy(out_host, out, 24, hipMemcpyDeviceToHost);
+  (void)hipFree(flag);
+  (void)hipFree(out);
+  return e;
+}
+
+}  // extern "C"

@@ -1,14 +1,14 @@
 // Persistent decode runtime for gfx950 (MI355X) and the C ABI of include/fleet_mi355x.h.
 //
-// One launch of 256 workgroups, one per CU (the 96 KiB of dynamic LDS each admits one per CU), with
-// blockIdx b on XCD b % 8 (checked at fx_create). Rank 0 of each XCD (blocks 0..7) is that XCD's
-// scheduler: it aggregates the epoch flags of the XCD's 31 workers and, for a device-wide sync,
-// exchanges one flag per XCD with the other seven schedulers, then releases its workers. The
-// workers (blocks 8..255) walk the task table, iteration by iteration, running their share of each
-// stage (fx_ops.h) and announcing completion through their own flag. No counter is shared by more
-// than one writer (same-address atomics serialise at ~150 ns each on this part) and no cache
-// maintenance instruction is issued: everything exchanged between workgroups travels through
-// sc1 (agent-coherent) loads and stores, ordered by s_waitcnt.
+// One cooperative launch of 256 workgroups, one per CU (the 96 KiB of dynamic LDS each admits one
+// per CU), with blockIdx b on XCD b % 8 (checked at fx_create). Every workgroup is a worker: it
+// walks the task table, iteration by iteration, and runs its share of each stage (fx_ops.h). There
+// is no barrier between stages: each stage publishes its outputs as tagged packets
+// (fleet_mi355x.h, "dataflow") and each consumer polls only the packets it reads, after issuing its
+// own weight loads, so a stage starts as soon as its inputs exist and weight streaming overlaps the
+// wait. Values that are not packets (cache rows, attention partials) are stored with the sc1
+// policy and completed (s_waitcnt) before the packet that announces them. No counter is shared by
+// two writers and no cache-maintenance instruction is issued.
 //
 // Replaces the fork runtime's prepare / scheduler / worker kernels and event counters
 // (docs/fleet/03-runtime.md:125-313, fleet/patches/sched_xcd.patch) with a static task table.
@@ -22,12 +22,9 @@
 #include "fx_ops.h"
 
 #define FX_BLOCKS 256
-static_assert(sizeof(fx_stage) == 200, "fx_stage layout is part of the ABI (fleet/runtime.py FxStage)");
-#define FX_WORKERS 248
-#define FX_XWORKERS 31
-// a wait that has not been satisfied after this many s_memrealtime ticks (100 MHz) declares the
-// run failed: every wait then returns, so the grid drains instead of hanging
-#define FX_WAIT_TICKS (200ull * 1000 * 1000)
+static_assert(sizeof(fx_stage) == 208, "fx_stage layout is part of the ABI (fleet/runtime.py FxStage)");
+static_assert(FX_BLOCKS == FX_WORKERS, "one worker per CU");
+#define FX_ERR_WORDS 64
 
 struct FxRunArgs {
   const fx_stage* stages;
@@ -36,89 +33,33 @@ struct FxRunArgs {
   int n_epi;
   int iters, step0, n_prompt;
   int64_t* tokens;
-  uint32_t* sync;
+  uint32_t* err;
   uint64_t* timing;
-  uint64_t* prof;      // [n_stages][256][2] stamps of iteration prof_iter, or null
+  uint64_t* prof;      // [n_stages][256][FX_PROF_SLOTS] stamps of iteration prof_iter, or null
   int prof_iter;
   uint32_t epoch0;
 };
 
-__device__ __forceinline__ bool timed_out(uint64_t t0, uint32_t* sync) {
-  if (__builtin_amdgcn_s_memrealtime() - t0 > FX_WAIT_TICKS) {
-    flag_st(&sync[FX_FLAG_ERROR], 1u);
-    return true;
-  }
-  return flag_ld(&sync[FX_FLAG_ERROR]) != 0u;
-}
-
-// worker side of a sync: publish the epoch, wait for the scheduler's go
-__device__ __forceinline__ void worker_sync(uint32_t* sync, int b, uint32_t epoch) {
-  wait_mem();
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    flag_st(&sync[FX_FLAG_ARRIVE(b)], epoch);
-    uint64_t t0 = __builtin_amdgcn_s_memrealtime();
-    uint32_t spins = 0;
-    while (flag_ld(&sync[FX_FLAG_GO(b)]) < epoch) {
-      if ((++spins & 255u) == 0 && timed_out(t0, sync)) break;
-    }
-  }
-  __syncthreads();
-}
-
-// scheduler side (wave 0 of block x): gather the XCD's workers, optionally all XCDs, release
-__device__ __forceinline__ void scheduler_sync(uint32_t* sync, int x, uint32_t epoch, bool global) {
-  const int lane = lane_id();
-  const int wb = (lane + 1) * 8 + x;   // block of worker `lane` of this XCD (lane < 31)
-  uint64_t t0 = __builtin_amdgcn_s_memrealtime();
-  uint32_t spins = 0;
-  bool ok;
-  do {
-    ok = lane >= FX_XWORKERS || flag_ld(&sync[FX_FLAG_ARRIVE(wb)]) >= epoch;
-    ok = __all(ok);
-    if (!ok && (++spins & 63u) == 0 && timed_out(t0, sync)) break;
-  } while (!ok);
-  if (global) {
-    if (lane == 0) flag_st(&sync[FX_FLAG_XCD(x)], epoch);
-    do {
-      ok = lane >= FX_XCDS || flag_ld(&sync[FX_FLAG_XCD(lane)]) >= epoch;
-      ok = __all(ok);
-      if (!ok && (++spins & 63u) == 0 && timed_out(t0, sync)) break;
-    } while (!ok);
-  }
-  if (lane < FX_XWORKERS) flag_st(&sync[FX_FLAG_GO(wb)], epoch);
+__device__ __forceinline__ void env_init(FxEnv& env, char* lds, int64_t* tokens, uint32_t* err, int n_prompt) {
+  const int b = blockIdx.x;
+  env.worker = b;
+  env.nworkers = FX_WORKERS;
+  env.xcd = b & 7;
+  env.xrank = b >> 3;
+  env.xworkers = FX_XWORKERS;
+  env.n_prompt = n_prompt;
+  env.tokens = tokens;
+  env.err = err;
+  env.lds = lds;
+  env.pst = nullptr;
+  env.token = -1;
 }
 
 __device__ __forceinline__ void persistent_body(const FxRunArgs& a) {
   extern __shared__ __attribute__((aligned(16))) char lds[];
   const int b = blockIdx.x;
-  const int x = b & 7, rank = b >> 3;
-  if (rank == 0) {
-    if (wave_id() != 0) return;
-    uint32_t epoch = a.epoch0;
-    for (int it = 0; it < a.iters; ++it)
-      for (int s = 0; s < a.n_stages; ++s) {
-        const int sy = a.stages[s].sync;
-        if (sy != FX_SYNC_NONE) scheduler_sync(a.sync, x, ++epoch, sy == FX_SYNC_GLOBAL);
-      }
-    for (int s = 0; s < a.n_epi; ++s) {
-      const int sy = a.epi[s].sync;
-      if (sy != FX_SYNC_NONE) scheduler_sync(a.sync, x, ++epoch, sy == FX_SYNC_GLOBAL);
-    }
-    return;
-  }
   FxEnv env;
-  env.xcd = x;
-  env.xrank = rank - 1;
-  env.xworkers = FX_XWORKERS;
-  env.worker = env.xrank * 8 + x;
-  env.nworkers = FX_WORKERS;
-  env.n_prompt = a.n_prompt;
-  env.tokens = a.tokens;
-  env.sync = a.sync;
-  env.lds = lds;
-  env.moe_e = -1;
-  uint32_t epoch = a.epoch0;
+  env_init(env, lds, a.tokens, a.err, a.n_prompt);
   // the current stage descriptor is staged in LDS (read by every wave, never spilled to scratch)
   fx_stage* sst = (fx_stage*)(lds + LDS_STAGE);
   auto stage_in = [&](const fx_stage* src) {
@@ -129,31 +70,33 @@ __device__ __forceinline__ void persistent_body(const FxRunArgs& a) {
   for (int it = 0; it < a.iters; ++it) {
     env.iter = it;
     env.step = a.step0 + it;
-    if (env.worker == 0 && threadIdx.x == 0 && a.timing) a.timing[it] = __builtin_amdgcn_s_memrealtime();
+    env.tbase = a.epoch0 + (uint32_t)(it * a.n_stages);
+    env.token = -1;
+    if (b == 0 && threadIdx.x == 0 && a.timing) a.timing[it] = __builtin_amdgcn_s_memrealtime();
     const bool prof = a.prof && it == a.prof_iter;
     for (int s = 0; s < a.n_stages; ++s) {
       stage_in(a.stages + s);
-      const int sync_kind = sst->sync;
-      const bool skip = (sst->flags & FX_F_HEAD) && (env.step + 1 < env.n_prompt);
-      if (prof && threadIdx.x == 0) a.prof[((size_t)s * FX_BLOCKS + b) * 2] = __builtin_amdgcn_s_memrealtime();
-      if (!skip) run_stage(*sst, env);
+      if ((sst->flags & FX_F_HEAD) && (env.step + 1 < env.n_prompt)) continue;
+      env.sidx = s;
+      env.pst = prof ? a.prof + ((size_t)s * FX_BLOCKS + b) * FX_PROF_SLOTS : nullptr;
+      prof_mark(env, 0);
+      run_stage(*sst, env);
       if (prof) {
-        wait_mem();
         __syncthreads();
-        if (threadIdx.x == 0) a.prof[((size_t)s * FX_BLOCKS + b) * 2 + 1] = __builtin_amdgcn_s_memrealtime();
+        prof_mark(env, 3);
       }
-      if (sync_kind != FX_SYNC_NONE) worker_sync(a.sync, b, ++epoch);
     }
   }
-  env.iter = a.iters - 1;
+  env.pst = nullptr;
+  env.iter = a.iters;
   env.step = a.step0 + a.iters - 1;
+  env.tbase = a.epoch0 + (uint32_t)(a.iters * a.n_stages);
   for (int s = 0; s < a.n_epi; ++s) {
     stage_in(a.epi + s);
-    const int sync_kind = sst->sync;
+    env.sidx = a.n_stages + s;
     run_stage(*sst, env);
-    if (sync_kind != FX_SYNC_NONE) worker_sync(a.sync, b, ++epoch);
   }
-  if (env.worker == 0 && threadIdx.x == 0 && a.timing) a.timing[a.iters] = __builtin_amdgcn_s_memrealtime();
+  if (b == 0 && threadIdx.x == 0 && a.timing) a.timing[a.iters] = __builtin_amdgcn_s_memrealtime();
 }
 
 // The decode launch (iterations that end in the LM head + argmax) and the prefill launch (prompt
@@ -162,26 +105,18 @@ __device__ __forceinline__ void persistent_body(const FxRunArgs& a) {
 __global__ void __launch_bounds__(FX_THREADS) fx_persistent(FxRunArgs a) { persistent_body(a); }
 __global__ void __launch_bounds__(FX_THREADS) fx_prefill(FxRunArgs a) { persistent_body(a); }
 
-// one stage as a standalone launch (kernel suite): same work split, no syncs
-__global__ void __launch_bounds__(FX_THREADS) fx_stage_kernel(fx_stage st, int step, int iter, int n_prompt,
-                                                            int64_t* tokens, uint32_t* sync) {
+// one stage as a standalone launch (kernel suite): same work split; packet inputs carry
+// tbase + src[k] + 1, outputs tbase + sidx + 1
+__global__ void __launch_bounds__(FX_THREADS) fx_stage_kernel(fx_stage st, int step, int n_prompt, uint32_t tbase, int sidx,
+                                                            int64_t* tokens, uint32_t* err) {
   extern __shared__ __attribute__((aligned(16))) char lds[];
-  const int b = blockIdx.x;
-  const int x = b & 7, rank = b >> 3;
-  if (rank == 0) return;
   FxEnv env;
-  env.xcd = x;
-  env.xrank = rank - 1;
-  env.xworkers = FX_XWORKERS;
-  env.worker = env.xrank * 8 + x;
-  env.nworkers = FX_WORKERS;
-  env.n_prompt = n_prompt;
-  env.tokens = tokens;
-  env.sync = sync;
-  env.lds = lds;
-  env.moe_e = -1;
-  env.iter = iter;
+  env_init(env, lds, tokens, err, n_prompt);
+  env.iter = 0;
   env.step = step;
+  env.tbase = tbase;
+  env.sidx = sidx;
+  if (tokens) env.token = tokens[step];
   run_stage(st, env);
 }
 
@@ -300,7 +235,7 @@ struct fx_ctx {
   int device;
   int cus;
   std::string err;
-  uint32_t* sync = nullptr;
+  uint32_t* err_flag = nullptr;
   uint64_t* timing = nullptr;
   int timing_cap = 0;
   int last_iters = 0;
@@ -354,8 +289,8 @@ int fx_create(int device, fx_ctx** out) {
   HIPCHK(c, hipFuncSetAttribute((const void*)fx_prefill, hipFuncAttributeMaxDynamicSharedMemorySize, FX_LDS_BYTES));
   HIPCHK(c, hipFuncSetAttribute((const void*)fx_stage_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, FX_LDS_BYTES));
   HIPCHK(c, hipFuncSetAttribute((const void*)fx_xcc_map, hipFuncAttributeMaxDynamicSharedMemorySize, FX_LDS_BYTES));
-  HIPCHK(c, hipMalloc(&c->sync, FX_SYNC_WORDS * 4));
-  HIPCHK(c, hipMemset(c->sync, 0, FX_SYNC_WORDS * 4));
+  HIPCHK(c, hipMalloc(&c->err_flag, FX_ERR_WORDS * 4));
+  HIPCHK(c, hipMemset(c->err_flag, 0, FX_ERR_WORDS * 4));
   c->timing_cap = FX_MAX_ITERS + 1;
   HIPCHK(c, hipMalloc(&c->timing, sizeof(uint64_t) * c->timing_cap));
   HIPCHK(c, hipEventCreate(&c->ev0));
@@ -376,7 +311,7 @@ int fx_create(int device, fx_ctx** out) {
 
 int fx_destroy(fx_ctx* c) {
   if (!c) return FX_OK;
-  if (c->sync) (void)hipFree(c->sync);
+  if (c->err_flag) (void)hipFree(c->err_flag);
   if (c->timing) (void)hipFree(c->timing);
   if (c->d_stages) (void)hipFree(c->d_stages);
   if (c->d_epi) (void)hipFree(c->d_epi);
@@ -429,24 +364,26 @@ int fx_synchronize(fx_ctx* c) {
 }
 
 // host-side checks of one stage against what its device code assumes
-static int check_stage(fx_ctx* c, const fx_stage& s, int idx) {
+static int check_stage(fx_ctx* c, const fx_stage& s, int idx, int n_total) {
   auto bad = [&](const std::string& m) { return fail(c, FX_E_ARG, "stage " + std::to_string(idx) + ": " + m); };
-  if (s.sync < FX_SYNC_NONE || s.sync > FX_SYNC_GLOBAL) return bad("sync kind");
+  for (int k = 0; k < 4; ++k)
+    if (s.src[k] < -n_total || s.src[k] >= n_total) return bad("packet source out of range");
   switch (s.op) {
     case FX_OP_GEMV: {
       if (!s.w || !s.out || s.n_rows <= 0 || s.k <= 0 || s.k % 8) return bad("gemv shape/pointers");
       const int nj = (s.k / 8 + 63) / 64;
       if (!(nj <= 4 || nj == 22)) return bad("gemv K not supported: " + std::to_string(s.k));
-      if (s.k > 11264) return bad("gemv K exceeds LDS row");
-      if (s.in_kind == FX_IN_VEC && !s.x) return bad("gemv input");
-      if (s.in_kind == FX_IN_EMBED && (!s.aux[0] || !s.aux[3])) return bad("embed table / amax");
-      if (s.in_kind == FX_IN_COMBINE && (!s.x || !s.aux[0] || !s.aux[1] || s.n_slots <= 0 || s.n_slots > 16))
-        return bad("combine inputs");
+      if (s.k > 11264) return bad("gemv K exceeds the LDS row");
+      if (s.in_kind == FX_IN_VEC && (!s.x || s.k % 4)) return bad("gemv input");
+      if (s.in_kind == FX_IN_EMBED && (!s.aux[0] || !s.aux[3] || !s.aux[4])) return bad("embed table / amax / tokens");
       if ((s.flags & FX_F_NORM) && !s.w_norm) return bad("norm weight");
       if ((s.flags & FX_F_RESIDUAL) && !s.res) return bad("residual");
-      if ((s.flags & FX_F_RESIDUAL) && (s.n_rows + FX_WORKERS - 1) / FX_WORKERS > FX_MAX_RES_ROWS)
-        return bad("residual rows per worker exceed the LDS table");
-      if ((s.flags & FX_F_WRITE_X) && !s.aux[2]) return bad("x_out");
+      if ((s.flags & FX_F_RES_EMBED) && !s.aux[0]) return bad("embedding residual");
+      const int groups = (s.n_rows + 3) / 4;
+      const int rows_max = 4 * ((groups + FX_WORKERS - 1) / FX_WORKERS);
+      if ((s.flags & (FX_F_OUT_LL | FX_F_RESIDUAL | FX_F_RES_EMBED)) && rows_max > FX_MAX_OUT_ROWS / 2)
+        return bad("rows per worker exceed the LDS row table");
+      if ((s.flags & FX_F_OUT_LL) && s.n_rows % 4) return bad("packet output needs rows in multiples of 4");
       if ((s.flags & FX_F_ARGMAX) && !s.aux[3]) return bad("amax");
       break;
     }
@@ -455,35 +392,38 @@ static int check_stage(fx_ctx* c, const fx_stage& s, int idx) {
     case FX_OP_MLA_MERGE_UV:
       if (s.n_rows != 16 || s.d_c != 512 || s.d_r != 64 || s.d_n != 128) return bad("MLA dims must be 16 x (512, 64, 128)");
       if (!s.x || !s.out || (s.op != FX_OP_MLA_ATTEND && !s.w)) return bad("MLA pointers");
-      if (s.op == FX_OP_MLA_PREP && (!s.aux[0] || !s.aux[1] || !s.aux[2] || !s.aux[3] || !s.aux[4] || !s.w_norm))
+      if (s.op == FX_OP_MLA_PREP && (!s.aux[0] || !s.aux[1] || !s.aux[2] || !s.aux[3] || !s.aux[4] || !s.aux[5] || !s.w_norm))
         return bad("prep pointers");
       if (s.op == FX_OP_MLA_ATTEND) {
-        if (!s.aux[0] || !s.aux[1] || !s.aux[2] || !s.aux[4]) return bad("attend pointers");
-        if (s.split <= 0 || s.n_splits <= 0 || s.prow < s.d_c + 1) return bad("attend splits");
-        if (s.n_splits * s.split < s.s_max) return bad("splits do not cover s_max");
-        if (2 * s.n_splits * 4 > 37 * 1024) return bad("too many splits for the merge table");
+        if (!s.aux[0] || !s.aux[1] || !s.aux[2] || !s.aux[5] || !s.aux[6]) return bad("attend pointers");
+        if (s.split <= 0 || s.split % 32 || s.n_splits <= 0 || s.prow < s.d_c + 1 || s.prow % 4) return bad("attend splits");
+        if ((long long)s.n_splits * s.split < s.s_max) return bad("splits do not cover s_max");
+      }
+      if (s.op == FX_OP_MLA_MERGE_UV) {
+        if (!s.aux[6] || s.split <= 0) return bad("merge pointers");
+        if (s.n_splits * 4 > 37 * 1024) return bad("too many splits for the merge table");
       }
       break;
     case FX_OP_MOE_ROUTER:
-      if (!s.w || !s.x || !s.out || !s.w_norm || s.n_rows > 64 || s.k != 2048) return bad("router");
+      if (!s.w || !s.x || !s.out || !s.w_norm || s.n_rows > 64 || s.n_rows % 2 || s.k != 2048) return bad("router");
       break;
     case FX_OP_MOE_W13:
-      if (!s.w || !s.x || !s.out || !s.w_norm || !s.aux[0] || !s.aux[1] || !s.aux[2] || !s.aux[3] || !s.aux[4] ||
-          !s.aux[7])
+      if (!s.w || !s.x || !s.out || !s.w_norm || !s.aux[0] || !s.aux[1] || !s.aux[2] || !s.aux[3] || !s.aux[4])
         return bad("w13 pointers");
-      if (s.n_slots != FX_XCDS || s.topk + s.n_forced != s.n_slots || s.aux_i0 > 64 || s.k != 2048) return bad("w13 shape");
+      if (s.n_slots != FX_XCDS || s.topk + s.n_forced != s.n_slots || s.aux_i0 > 64 || s.aux_i0 % 2 || s.k != 2048 ||
+          s.n_rows % 4 || (s.n_rows / 2) % FX_XWORKERS)
+        return bad("w13 shape");
       break;
     case FX_OP_MOE_W2:
-      if (!s.w || !s.x || !s.out || !s.aux[7] || (s.k / 8 + 63) / 64 > 3) return bad("w2");
-      break;
-    case FX_OP_MOE_COMBINE:
-      if (!s.x || !s.out || !s.aux[0] || !s.aux[1] || s.n_rows % 8) return bad("combine");
+      if (!s.w || !s.x || !s.out || !s.res || !s.aux[0] || (s.k / 8 + 63) / 64 > 3 || s.k % 8) return bad("w2");
+      if (s.n_slots != FX_XCDS || s.topk + s.n_forced != s.n_slots || s.aux_i0 > 64 || s.aux_i0 % 2) return bad("w2 slots");
+      if (s.n_rows != 8 * FX_WORKERS || s.n_slots * s.k > 11264) return bad("w2 rows / input row");
       break;
     case FX_OP_DENSE_GU:
-      if (!s.w || !s.x || !s.out || !s.w_norm || s.k != 2048) return bad("dense gate/up");
+      if (!s.w || !s.x || !s.out || !s.w_norm || s.k != 2048 || s.n_rows % 2) return bad("dense gate/up");
       break;
     case FX_OP_ARGMAX:
-      if (!s.aux[3]) return bad("argmax");
+      if (!s.aux[3] || !s.aux[4]) return bad("argmax");
       break;
     default:
       return bad("unknown op " + std::to_string(s.op));
@@ -495,11 +435,11 @@ int fx_load_plan(fx_ctx* c, const fx_stage* st, int32_t n, const fx_stage* epi, 
   if (!c) return FX_E_ARG;
   if (n <= 0 || !st) return fail(c, FX_E_ARG, "empty plan");
   for (int i = 0; i < n; ++i) {
-    int r = check_stage(c, st[i], i);
+    int r = check_stage(c, st[i], i, n);
     if (r) return r;
   }
   for (int i = 0; i < n_epi; ++i) {
-    int r = check_stage(c, epi[i], n + i);
+    int r = check_stage(c, epi[i], n + i, n);
     if (r) return r;
   }
   if (c->d_stages) { HIPCHK(c, hipFree(c->d_stages)); c->d_stages = nullptr; }
@@ -524,18 +464,10 @@ int fx_launch(fx_ctx* c, int32_t iters, int32_t step0, int32_t n_prompt, int64_t
   for (const fx_stage& s : c->h_stages) {
     if (s.s_max > 0 && step0 + iters > s.s_max) return fail(c, FX_E_ARG, "steps exceed the cache length s_max");
   }
-  int syncs = 0;
-  for (const fx_stage& s : c->h_stages) syncs += s.sync != FX_SYNC_NONE;
-  int syncs_epi = 0;
-  for (const fx_stage& s : c->h_epi) syncs_epi += s.sync != FX_SYNC_NONE;
-  const uint64_t total = (uint64_t)syncs * iters + syncs_epi;
+  const uint64_t total = (uint64_t)c->n_stages * (uint64_t)iters;
   hipStream_t s = (hipStream_t)stream;
-  if ((uint64_t)c->epoch + total > 0xF0000000ull) {
-    // flags restart from zero: wait for every launch still using them
-    HIPCHK(c, hipStreamSynchronize(s));
-    HIPCHK(c, hipMemset(c->sync, 0, FX_SYNC_WORDS * 4));
-    c->epoch = 0;
-  }
+  if ((uint64_t)c->epoch + total + (uint64_t)c->n_stages + 1 > 0xFFFFFFF0ull)
+    return fail(c, FX_E_STATE, "packet tags exhausted for this context: recreate it and zero the plan's packet buffers");
   FxRunArgs a;
   a.stages = c->d_stages;
   a.n_stages = c->n_stages;
@@ -545,12 +477,12 @@ int fx_launch(fx_ctx* c, int32_t iters, int32_t step0, int32_t n_prompt, int64_t
   a.step0 = step0;
   a.n_prompt = n_prompt;
   a.tokens = tokens;
-  a.sync = c->sync;
+  a.err = c->err_flag;
   a.timing = c->timing;
   a.prof = nullptr;
   a.prof_iter = -1;
   if (c->prof_iter >= 0 && c->prof_iter < iters) {
-    const size_t words = (size_t)c->n_stages * FX_BLOCKS * 2;
+    const size_t words = (size_t)c->n_stages * FX_BLOCKS * FX_PROF_SLOTS;
     if (c->prof_words < words) {
       HIPCHK(c, hipStreamSynchronize(s));
       if (c->prof) HIPCHK(c, hipFree(c->prof));
@@ -578,7 +510,7 @@ int fx_finish(fx_ctx* c, void* stream) {
   if (!c) return FX_E_ARG;
   HIPCHK(c, hipStreamSynchronize((hipStream_t)stream));
   uint32_t err = 0;
-  HIPCHK(c, hipMemcpy(&err, c->sync + FX_FLAG_ERROR, 4, hipMemcpyDeviceToHost));
+  HIPCHK(c, hipMemcpy(&err, c->err_flag, 4, hipMemcpyDeviceToHost));
   if (err) return fail(c, FX_E_STATE, "a synchronisation wait timed out inside the persistent kernel; create a new context");
   return FX_OK;
 }
@@ -612,7 +544,7 @@ int fx_set_profile(fx_ctx* c, int32_t iter) {
 int fx_read_profile(fx_ctx* c, uint64_t* buf, int32_t n) {
   if (!c || !buf) return -1;
   if (!c->prof) return 0;
-  size_t m = (size_t)c->n_stages * FX_BLOCKS * 2;
+  size_t m = (size_t)c->n_stages * FX_BLOCKS * FX_PROF_SLOTS;
   if ((size_t)n < m) m = (size_t)n;
   if (hipMemcpy(buf, c->prof, m * 8, hipMemcpyDeviceToHost) != hipSuccess) return -1;
   return (int)m;
@@ -634,17 +566,22 @@ int fx_read_timing(fx_ctx* c, uint64_t* buf, int32_t n) {
   return m;
 }
 
-int fx_run_stage(fx_ctx* c, const fx_stage* st, int32_t step, int32_t iter, void* stream) {
+int fx_run_stage(fx_ctx* c, const fx_stage* st, int32_t step, uint32_t tbase, int32_t sidx, void* stream) {
   if (!c || !st) return FX_E_ARG;
-  int r = check_stage(c, *st, 0);
+  int r = check_stage(c, *st, 0, 1 << 20);
   if (r) return r;
   hipStream_t s = (hipStream_t)stream;
   // the embed prologue reads tokens[step]; the argmax reduce always stores tokens[step + 1]
   const int n_prompt = st->op == FX_OP_ARGMAX ? 0 : (1 << 30);
-  hipLaunchKernelGGL(fx_stage_kernel, dim3(FX_BLOCKS), dim3(FX_THREADS), FX_LDS_BYTES, s, *st, step, iter, n_prompt,
-                     (int64_t*)st->aux[4], c->sync);
-  HIPCHK(c, hipGetLastError());
+  const bool uses_tokens = st->op == FX_OP_ARGMAX ||
+                           (st->op == FX_OP_GEMV && (st->in_kind == FX_IN_EMBED || (st->flags & FX_F_RES_EMBED)));
+  int64_t* tokens = uses_tokens ? (int64_t*)st->aux[4] : nullptr;
+  void* args[] = {(void*)st, &step, (void*)&n_prompt, &tbase, &sidx, &tokens, &c->err_flag};
+  HIPCHK(c, hipLaunchCooperativeKernel((const void*)fx_stage_kernel, dim3(FX_BLOCKS), dim3(FX_THREADS), args, FX_LDS_BYTES, s));
   HIPCHK(c, hipStreamSynchronize(s));
+  uint32_t err = 0;
+  HIPCHK(c, hipMemcpy(&err, c->err_flag, 4, hipMemcpyDeviceToHost));
+  if (err) return fail(c, FX_E_STATE, "a packet wait timed out in the stage launch; create a new context");
   return FX_OK;
 }
 

@@ -3,15 +3,16 @@
 The reference attaches every tensor to a mirage PersistentKernel, issues one mpk.<op>_layer per
 call and JIT-compiles the worker switch. Here the tensors are device buffers the host owns
 (fleet.runtime.DeviceBuffer), each call becomes one fx_stage (include/fleet_mi355x.h), and the table
-is validated and uploaded by fx_load_plan -- no code generation. Three calls are folded into the input
-prologue of the GEMV that follows them (no sync of their own):
+is validated and uploaded by fx_load_plan -- no code generation. Three calls are folded into a
+neighbour (no stage of their own):
   prologue.embed     -> L0.qkva reads W_embed[tokens[step]] (or, once past the prompt, the previous
-                        head's argmax) and worker 0 writes x_res;
-  L{l}.combine       -> the next GEMV (L{l+1}.qkva or head.lm_head) computes x_res + sum w_s out8[s]
-                        itself and worker 0 writes it to the other x_res buffer (two physical x_res
-                        buffers alternate, so no stage reads and writes the same one);
-  head.argmax_reduce -> the next iteration's embed prologue; the last iteration's runs as the epilogue.
-A truncated plan (--stop-after) that ends on a combine runs it as a standalone stage.
+                        head's argmax); L0.o_proj takes the same row as its residual;
+  L{l}.combine       -> L{l}.w2: each worker computes its 8 output rows for every slot and combines
+                        them with the residual;
+  head.argmax_reduce -> the next iteration's embed; the last iteration's runs as the epilogue.
+Every packet input of a stage names the stage that produces it (fx_stage.src): the last writer
+before it in the table, or, for the head's argmax read by the next iteration's embed, a stage of
+the previous iteration (a negative index).
 """
 import numpy as np
 
@@ -21,8 +22,8 @@ from fleet.pack_weights import Dims, REAL_DIMS, XCDS, rope_tables
 
 
 def make_tensors(rt, plan, packed, capture, meta):
-    """name -> DeviceBuffer: `new` tensors allocated and zeroed, inputs taken from packed weights,
-    the captured cache/tables and the meta tensors (shapes checked)."""
+    """name -> DeviceBuffer: `new` tensors allocated and zeroed (packet tensors start at tag 0),
+    inputs taken from packed weights, the captured cache/tables and the meta tensors (shapes checked)."""
     host = {}
     for name, t in plan.tensors.items():
         if t.kind == "new":
@@ -32,7 +33,6 @@ def make_tensors(rt, plan, packed, capture, meta):
         src = {"weight": packed, "capture": capture, "meta": meta}[kind][key]
         assert tuple(src.shape) == tuple(t.shape), (name, src.shape, t.shape)
         host[name] = src
-    host["x_res_b"] = rt.alloc((plan.dims.H,), "bf16").zero()
     return host
 
 
@@ -41,24 +41,18 @@ def _stage(**kw):
 
 
 def compile_stages(plan, host):
-    """(stages, epilogue, x_final): the fx_stage table of one iteration, the post-loop stages, and the
-    name of the physical buffer that holds x_res after the last call."""
+    """(stages, epilogue): the fx_stage table of one iteration and the post-loop stages. Each stage's
+    packet inputs are resolved to their producing stage (src)."""
     d = plan.dims
-    cur, other = "x_res", "x_res_b"
-    stages, epi = [], []
-    labels = []
-    pend_embed = pend_combine = None
-    sync_of = {G.GLOBAL: R.FX_SYNC_GLOBAL, G.XCD: R.FX_SYNC_XCD, G.NONE: R.FX_SYNC_NONE}
+    stages, epi, labels = [], [], []
+    reads = []          # per stage: [(src slot, tensor name)]
+    pend_embed = None
     B = lambda n: host[n].ptr if n else 0
 
-    def xr(name):
-        return cur if name == "x_res" else name
-
-    def standalone_combine(c):
-        stages.append(_stage(op=R.FX_OP_MOE_COMBINE, sync=R.FX_SYNC_GLOBAL, n_rows=d.H, n_slots=d.N_SLOTS,
-                             x=B(cur), out=B(cur), aux={0: B(c.args["input"]), 1: B(c.args["weight"])},
-                             layer=int(c.label.split(".")[0][1:])))
-        labels.append(c.label)
+    def add(st, label, ins):
+        stages.append(st)
+        labels.append(label)
+        reads.append(ins)
 
     for c in plan.calls:
         a = c.args
@@ -67,114 +61,144 @@ def compile_stages(plan, host):
             pend_embed = c
             continue
         if m == "moe_mul_sum_add_layer":
-            pend_combine = c
+            assert stages and stages[-1].op == R.FX_OP_MOE_W2, "combine must follow its w2"
             continue
         if m == "argmax_reduce_layer":
-            epi.append(_stage(op=R.FX_OP_ARGMAX, sync=R.FX_SYNC_NONE, aux={3: B(a["input"]), 4: B("tokens")}))
+            epi.append((_stage(op=R.FX_OP_ARGMAX, aux={3: B(a["input"]), 4: B("tokens")}), [(0, a["input"])]))
             continue
         layer = int(c.label.split(".")[0][1:]) if c.label.startswith("L") else -1
-        sync = sync_of[c.sync]
+        common = dict(layer=layer, eps=plan.eps)
         if m == "linear_gemv_layer":
             W = host[a["weight"]]
-            st = _stage(op=R.FX_OP_GEMV, sync=sync, layer=layer, n_rows=W.shape[0], k=W.shape[1], eps=plan.eps,
-                        w=W.ptr, out=B(xr(a["output"])), in_kind=R.FX_IN_VEC)
+            st = _stage(op=R.FX_OP_GEMV, n_rows=W.shape[0], k=W.shape[1], w=W.ptr, out=B(a["output"]),
+                        in_kind=R.FX_IN_VEC, **common)
+            ins = []
             flags = 0
+            if host[a["output"]].dtype == "pk16":
+                flags |= R.FX_F_OUT_LL
             if a.get("norm"):
                 flags |= R.FX_F_NORM
                 st.w_norm = B(a["w_norm"])
-            if a.get("residual"):
-                flags |= R.FX_F_RESIDUAL
-                st.res = B(xr(a["residual"]))
             if a.get("amax"):
                 flags |= R.FX_F_ARGMAX | R.FX_F_HEAD
                 st.aux[3] = B(a["amax"])
             lab = c.label
-            if pend_embed is not None and a["input"] == "x_res":
+            if pend_embed is not None and a["input"] == pend_embed.args["output"]:
                 lab = c.label + "+embed"
                 st.in_kind = R.FX_IN_EMBED
                 st.aux[0] = B("W_embed")
                 st.aux[3] = B("amax")
                 st.aux[4] = B("tokens")
-                st.aux[2] = B(cur)
-                flags |= R.FX_F_WRITE_X
+                ins.append((1, "amax"))
+                embed_out = pend_embed.args["output"]
                 pend_embed = None
-            elif pend_combine is not None and a["input"] == "x_res":
-                lab = c.label + "+combine"
-                st.in_kind = R.FX_IN_COMBINE
-                st.x = B(cur)
-                st.aux[0] = B(pend_combine.args["input"])
-                st.aux[1] = B(pend_combine.args["weight"])
-                st.n_slots = d.N_SLOTS
-                st.aux[2] = B(other)
-                flags |= R.FX_F_WRITE_X
-                cur, other = other, cur
-                pend_combine = None
             else:
-                if pend_combine is not None:
-                    standalone_combine(pend_combine)
-                    pend_combine = None
-                st.x = B(xr(a["input"]))
-            if st.out == B("x_res") or st.out == B("x_res_b"):
-                st.out = B(cur)
-            if st.res:
-                st.res = B(cur)
+                st.x = B(a["input"])
+                ins.append((0, a["input"]))
+            if a.get("residual"):
+                if layer == 0 and a["residual"] == "x_res" and plan.calls[0].method == "embed_layer":
+                    # layer 0's residual stream is the embedding row itself
+                    flags |= R.FX_F_RES_EMBED
+                    st.aux[0] = B("W_embed")
+                    st.aux[4] = B("tokens")
+                else:
+                    flags |= R.FX_F_RESIDUAL
+                    st.res = B(a["residual"])
+                    ins.append((2, a["residual"]))
             st.flags = flags
-            stages.append(st)
-            labels.append(lab)
+            add(st, lab, ins)
             continue
         assert pend_embed is None, "prologue.embed must be followed by L0.qkva"
-        if pend_combine is not None:
-            standalone_combine(pend_combine)
-            pend_combine = None
-        common = dict(sync=sync, layer=layer, eps=plan.eps)
         if m == "mla_prep_layer":
             st = _stage(op=R.FX_OP_MLA_PREP, n_rows=d.NH, d_c=d.D_C, d_r=d.D_R, d_n=d.D_N, s_max=plan.s_max,
                         x=B(a["qkva"]), w=B(a["w_uk"]), w_norm=B(a["w_kv_norm"]), out=B(a["ql_nope"]),
-                        aux={0: B(a["c_kv"]), 1: B(a["k_pe"]), 2: B(a["q_pe"]), 3: B(a["cos"]), 4: B(a["sin"])},
-                        **common)
+                        aux={0: B(a["c_kv"]), 1: B(a["k_pe"]), 2: B(a["q_pe"]), 3: B(a["cos"]), 4: B(a["sin"]),
+                             5: B(a["crow"])}, **common)
+            ins = [(0, a["qkva"])]
         elif m == "mla_attend_layer":
             st = _stage(op=R.FX_OP_MLA_ATTEND, n_rows=d.NH, d_c=d.D_C, d_r=d.D_R, d_n=d.D_N, split=a["split"],
-                        n_splits=a["n_splits"], prow=G.partials_row(d.D_C), s_max=plan.s_max, s_scores=plan.s_max,
+                        n_splits=a["n_splits"], prow=G.partials_row(d.D_C), s_max=plan.s_max,
                         scale=a["softmax_scale"], x=B(a["ql_nope"]), out=B(a["partials"]),
-                        aux={0: B(a["c_kv"]), 1: B(a["k_pe"]), 2: B(a["q_pe"]), 3: B(a.get("scores")),
-                             4: B(a["o_merged"])}, **common)
+                        aux={0: B(a["c_kv"]), 1: B(a["k_pe"]), 2: B(a["q_pe"]), 5: B(a["crow"]), 6: B(a["done"])},
+                        **common)
+            ins = [(0, a["ql_nope"])]
         elif m == "mla_merge_uv_layer":
-            st = _stage(op=R.FX_OP_MLA_MERGE_UV, n_rows=d.NH, d_c=d.D_C, d_r=d.D_R, d_n=d.D_V, x=B(a["input"]),
-                        w=B(a["w_uv"]), out=B(a["output"]), **common)
+            st = _stage(op=R.FX_OP_MLA_MERGE_UV, n_rows=d.NH, d_c=d.D_C, d_r=d.D_R, d_n=d.D_V, split=a["split"],
+                        n_splits=a["n_splits"], prow=G.partials_row(d.D_C), x=B(a["input"]), w=B(a["w_uv"]),
+                        out=B(a["output"]), aux={4: B(a.get("o_merged")), 6: B(a["done"])}, **common)
+            ins = [(0, a["done"])]
         elif m == "gang_linear_silu_layer":
-            st = _stage(op=R.FX_OP_DENSE_GU, n_rows=d.I_DENSE, k=d.H, x=B(cur), w_norm=B(a["w_norm"]),
+            st = _stage(op=R.FX_OP_DENSE_GU, n_rows=d.I_DENSE, k=d.H, x=B(a["input"]), w_norm=B(a["w_norm"]),
                         w=B(a["weight"]), out=B(a["output"]), aux={6: B(a.get("h"))}, **common)
+            ins = [(0, a["input"])]
         elif m == "moe_router_layer":
-            st = _stage(op=R.FX_OP_MOE_ROUTER, n_rows=d.E, k=d.H, topk=d.TOPK, x=B(cur), w_norm=B(a["w_norm"]),
+            st = _stage(op=R.FX_OP_MOE_ROUTER, n_rows=d.E, k=d.H, topk=d.TOPK, x=B(a["input"]), w_norm=B(a["w_norm"]),
                         w=B(a["w_gate"]), out=B(a["logits_x"]), **common)
+            ins = [(0, a["input"])]
         elif m == "gang_moe_w13_gemv_layer":
             rl = host[a["route_log"]]
             st = _stage(op=R.FX_OP_MOE_W13, n_rows=d.I_MOE, k=d.H, n_slots=d.N_SLOTS, topk=d.TOPK,
                         n_forced=d.N_SHARED, scaling=G.ROUTED_SCALING, aux_i0=d.E, aux_i1=rl.shape[1],
-                        prow=rl.shape[0], x=B(cur), w_norm=B(a["w_norm"]), w=B(a["weight"]), out=B(a["output"]),
+                        prow=rl.shape[0], x=B(a["input"]), w_norm=B(a["w_norm"]), w=B(a["weight"]), out=B(a["output"]),
                         aux={0: B(a["logits_x"]), 1: B(a["topk_w"]), 2: B(a["routing"]), 3: B(a["mask"]),
                              4: B(a["logits"]), 5: rl.ptr, 6: B(a["h"]), 7: B(a["sel"])}, **common)
+            ins = [(0, a["logits_x"]), (1, a["input"])]
         elif m == "gang_moe_w2_linear_layer":
-            st = _stage(op=R.FX_OP_MOE_W2, n_rows=d.H, k=d.I_MOE, x=B(a["input"]), w=B(a["weight"]),
-                        out=B(a["output"]), aux={7: B(a["sel"])}, **common)
+            comb = next(cc for cc in plan.calls if cc.label == c.label.replace(".w2", ".combine"))
+            st = _stage(op=R.FX_OP_MOE_W2, n_rows=d.H, k=d.I_MOE, n_slots=d.N_SLOTS, topk=d.TOPK, n_forced=d.N_SHARED,
+                        scaling=G.ROUTED_SCALING, aux_i0=d.E, x=B(a["input"]), w=B(a["weight"]),
+                        res=B(comb.args["residual"]), out=B(comb.args["output"]),
+                        aux={0: B(a["logits_x"]), 1: B(a["output"])}, **common)
+            ins = [(0, a["input"]), (1, a["logits_x"]), (2, comb.args["residual"])]
         else:
             raise ValueError(f"unknown plan method {m}")
-        stages.append(st)
-        labels.append(c.label)
+        add(st, c.label, ins)
     assert pend_embed is None, "a plan cannot end on prologue.embed"
-    if pend_combine is not None:
-        standalone_combine(pend_combine)
+    # resolve packet sources: the last writer before the stage, else the last writer of the table
+    # (previous iteration, negative index); a tensor with no writer gets -1 (never awaited: only the
+    # embed's amax when the plan has no head)
+    n = len(stages)
+    writer = {}
+    outputs = []
+    for i, st in enumerate(stages):
+        outs = {st.out}
+        if st.op == R.FX_OP_MLA_PREP:
+            outs |= {st.aux[2], st.aux[5]}
+        if st.op == R.FX_OP_MLA_ATTEND:
+            outs = {st.aux[6]}
+        if st.op == R.FX_OP_GEMV and st.flags & R.FX_F_ARGMAX:
+            outs.add(st.aux[3])
+        outputs.append(outs)
+    for i in range(n):
+        for k, name in reads[i]:
+            ptr = host[name].ptr
+            before = [j for j in range(i) if ptr in outputs[j]]
+            after = [j for j in range(i, n) if ptr in outputs[j]]
+            if before:
+                stages[i].src[k] = before[-1]
+            elif after:
+                stages[i].src[k] = after[-1] - n
+            else:
+                assert name == "amax", f"{labels[i]}: no stage writes {name}"
+                stages[i].src[k] = -1
+    epi_st = []
+    for st, ins in epi:
+        for k, name in ins:
+            ptr = host[name].ptr
+            w = [j for j in range(n) if ptr in outputs[j]]
+            st.src[k] = (w[-1] - n) if w else -1
+        epi_st.append(st)
     compile_stages.labels = labels
-    return stages, epi, cur
+    return stages, epi_st
 
 
 class Runner:
     """The built graph: rt + plan + host tensors + task table (what the reference's build() returns
     as (mpk, host, plan))."""
 
-    def __init__(self, rt, plan, host, stages, epi, x_final):
+    def __init__(self, rt, plan, host, stages, epi):
         self.rt, self.plan, self.host = rt, plan, host
-        self.stages, self.epi, self.x_final = stages, epi, x_final
+        self.stages, self.epi = stages, epi
         rt.load_plan(stages, epi)
 
     def run(self, iters, step0, n_prompt):
@@ -194,22 +218,28 @@ class Runner:
 
     def profile(self, iters, step0, n_prompt, iteration=0):
         """Run with per-stage stamps recorded for `iteration`; returns a list of per-stage dicts:
-        label, sync, start (us from the iteration's first stamp), busy (slowest worker's share),
-        spread (last minus first worker to finish), gap (until the next stage starts)."""
+        label, start (us from the iteration's first stamp), wait (slowest worker's arrival-to-inputs),
+        busy (slowest worker's inputs-to-outputs), end (last worker done, from the iteration start),
+        span (first start to last end)."""
         self.rt.set_profile(iteration)
         try:
             self.run(iters, step0, n_prompt)
         finally:
             self.rt.set_profile(-1)
-        st = self.rt.read_profile(len(self.stages))[:, 8:, :].astype(np.float64) / 100.0   # workers only, us
-        t0 = st[0, :, 0].min()
+        st = self.rt.read_profile(len(self.stages)).astype(np.float64) / 100.0   # us
+        t0 = st[0, :, 0][st[0, :, 0] > 0].min()
         rows = []
         for i, lab in enumerate(self.labels):
-            start, end = st[i, :, 0].min() - t0, st[i, :, 1].max() - t0
-            nxt = st[i + 1, :, 0].min() - t0 if i + 1 < len(self.labels) else end
-            busy = (st[i, :, 1] - st[i, :, 0]).max()
-            rows.append({"label": lab, "sync": int(self.stages[i].sync), "start": start, "busy": busy,
-                         "spread": st[i, :, 1].max() - st[i, :, 1].min(), "span": end - start, "gap": nxt - end})
+            s0, s1, s2, s3 = (st[i, :, k] for k in range(4))
+            ok = s0 > 0
+            if not ok.any():
+                rows.append({"label": lab, "start": 0.0, "wait": 0.0, "busy": 0.0, "end": 0.0, "span": 0.0})
+                continue
+            has_in = ok & (s1 > 0) & (s2 > 0)
+            wait = (s1[has_in] - s0[has_in]).max() if has_in.any() else 0.0
+            busy = (s2[has_in] - s1[has_in]).max() if has_in.any() else 0.0
+            rows.append({"label": lab, "start": s0[ok].min() - t0, "wait": wait, "busy": busy,
+                         "end": s3[ok].max() - t0, "span": s3[ok].max() - s0[ok].min()})
         return rows
 
     def timing_us(self):
@@ -217,7 +247,8 @@ class Runner:
         return np.diff(t.astype(np.float64)) / 100.0    # s_memrealtime ticks are 100 MHz
 
     def x_res(self):
-        return self.host[self.x_final].download()
+        """The residual stream after the last layer (bf16 bits)."""
+        return self.host["x_res"].download()
 
 
 def make_meta(rt, s_max, prompt):
@@ -250,8 +281,8 @@ def build(rt, packed, capture, meta, dims: Dims = REAL_DIMS, s_max=1056, layers=
     if stop_after:
         plan.truncate(stop_after)
     host = make_tensors(rt, plan, packed, capture, meta)
-    stages, epi, x_final = compile_stages(plan, host)
-    runner = Runner(rt, plan, host, stages, epi, x_final)
+    stages, epi = compile_stages(plan, host)
+    runner = Runner(rt, plan, host, stages, epi)
     runner.labels = list(compile_stages.labels)
     return runner
 
@@ -259,6 +290,6 @@ def build(rt, packed, capture, meta, dims: Dims = REAL_DIMS, s_max=1056, layers=
 def plan_json(plan):
     return {"dims": plan.dims.__dict__, "s_max": plan.s_max, "layers": plan.layers, "head": plan.head,
             "split": plan.split, "n_splits": plan.n_splits,
-            "calls": [{"method": c.method, "label": c.label, "sync": c.sync, "tasks": c.tasks,
+            "calls": [{"method": c.method, "label": c.label, "tasks": c.tasks,
                        "args": {k: v for k, v in c.args.items() if isinstance(v, (str, int, float, bool)) or v is None}}
                       for c in plan.calls]}

@@ -3,13 +3,13 @@
 A plan is a list of operator calls (method name, tensor names, parameters, label) plus the tensors to
 allocate or attach. The method names and labels are the reference's (L{l}.qkva, L{l}.mla_prep,
 L{l}.mla_attend, L{l}.mla_merge_uv, L{l}.o_proj, L{l}.router, L{l}.w13, L{l}.w2, L{l}.combine,
-head.lm_head, head.argmax_partial/argmax_reduce, prologue.embed) so --stop-after, the boundary dump
-and the compare keep their keys. What changes is the work split and the synchronisation each call
-carries: instead of the mirage event chain every call ends in one of
-  GLOBAL  all 248 workers (three flag hops through the per-XCD schedulers),
-  XCD     only the 31 workers of each XCD (one hop through that XCD's scheduler),
-and the attention, router and experts run per XCD (XCD x owns heads 2x, 2x+1 and MoE slot x), so
-four of the eight syncs of an MoE layer stay inside an XCD.
+head.lm_head, head.argmax_reduce, prologue.embed) so --stop-after, the boundary dump and the compare
+keep their keys. What changes is how calls hand data to each other: instead of the mirage event
+chain, every activation that crosses workgroups is a packet tensor (dtype pk16: bf16 values, two
+per 8-byte packet with the producer's tag; pk32: one f32 per packet), and each consumer waits on
+exactly the packets it reads. Attention runs per XCD (XCD x owns heads 2x, 2x+1), the MoE gate|up
+per slot (slot x on XCD x), everything else over all 256 workers. The residual stream alternates
+between two packet vectors, x_res (layer input) and x_mid (after attention).
 """
 import struct
 from dataclasses import dataclass, field
@@ -17,15 +17,13 @@ from dataclasses import dataclass, field
 from fleet.pack_weights import Dims, REAL_DIMS, XCDS
 
 SPLIT = 32                 # positions per attention split (the reference's D11); tiles of 32
-ARGMAX_SLICES = 248        # one partial argmax per worker
 N_FORCED = 2
 TOPK_TOTAL_SLOTS = 8
 SOFTMAX_SCALE = float(struct.unpack("<f", struct.pack("<f", 1.0 / 192 ** 0.5))[0])   # BASELINE: 1/sqrt(192)
 ROUTED_SCALING = 1.0
 RMS_EPS = 1e-6
-WORKERS = 248
-
-GLOBAL, XCD, NONE = "global", "xcd", "none"
+WORKERS = 256
+XWORKERS = WORKERS // XCDS
 
 
 def float_bits(x: float) -> int:
@@ -36,7 +34,7 @@ def float_bits(x: float) -> int:
 class Tensor:
     name: str
     shape: tuple
-    dtype: str = "bf16"           # bf16 | f32 | i32 | i64
+    dtype: str = "bf16"           # bf16 | f32 | i32 | i64 | pk16 | pk32 (packets)
     kind: str = "new"             # new | input (weights, captured cache, meta)
     source: str = ""
 
@@ -46,7 +44,6 @@ class Call:
     method: str
     args: dict
     tasks: int
-    sync: str = GLOBAL
     label: str = ""
     note: str = ""
 
@@ -54,9 +51,9 @@ class Call:
 OUTPUT_ARGS = {
     "embed_layer": ["output"],
     "linear_gemv_layer": ["output", "amax"],
-    "mla_prep_layer": ["c_kv", "k_pe", "ql_nope", "q_pe"],
-    "mla_attend_layer": ["partials", "o_merged", "scores"],
-    "mla_merge_uv_layer": ["output"],
+    "mla_prep_layer": ["c_kv", "k_pe", "ql_nope", "q_pe", "crow"],
+    "mla_attend_layer": ["partials", "done"],
+    "mla_merge_uv_layer": ["output", "o_merged"],
     "moe_router_layer": ["logits_x"],
     "gang_moe_w13_gemv_layer": ["output", "topk_w", "routing", "mask", "logits", "route_log", "h", "sel"],
     "gang_moe_w2_linear_layer": ["output"],
@@ -92,8 +89,8 @@ class Plan:
         self.tensors[name] = Tensor(name, tuple(shape), dtype, kind, source)
         return name
 
-    def op(self, method, tasks, sync=GLOBAL, label="", note="", **args):
-        self.calls.append(Call(method, args, tasks, sync, label, note))
+    def op(self, method, tasks, label="", note="", **args):
+        self.calls.append(Call(method, args, tasks, label, note))
 
     def index_of(self, label):
         for i, c in enumerate(self.calls):
@@ -102,8 +99,12 @@ class Plan:
         raise KeyError(label)
 
     def truncate(self, stop_label):
-        """Keep the calls up to and including the labelled one (the reference's --stop-after)."""
-        self.calls = self.calls[: self.index_of(stop_label) + 1]
+        """Keep the calls up to and including the labelled one (the reference's --stop-after). A w2
+        keeps its combine, which runs inside the same stage."""
+        i = self.index_of(stop_label)
+        if i + 1 < len(self.calls) and self.calls[i].method == "gang_moe_w2_linear_layer":
+            i += 1
+        self.calls = self.calls[: i + 1]
         return self
 
     def chain_violations(self):
@@ -143,7 +144,7 @@ def splits_for(s_max, split=SPLIT, n_splits=None):
 
 
 def build_plan(dims: Dims = REAL_DIMS, s_max: int = 1056, layers: int = 27, head: bool = True, split: int = SPLIT,
-               n_splits: int = None, iters_cap: int = 32, debug_scores: bool = False, softmax_scale: float = SOFTMAX_SCALE,
+               n_splits: int = None, iters_cap: int = 32, softmax_scale: float = SOFTMAX_SCALE,
                eps: float = RMS_EPS) -> Plan:
     d = dims
     assert 1 <= layers <= d.L
@@ -155,33 +156,34 @@ def build_plan(dims: Dims = REAL_DIMS, s_max: int = 1056, layers: int = 27, head
     # ---- meta and shared tensors
     p.t("tokens", (s_max + 1,), "i64", "input", "meta:tokens")
     p.t("W_embed", (d.V, d.H), kind="input", source="W_embed")
-    p.t("x_res", (d.H,))
-    p.t("qkva", (d.Q_OUT + d.KVA_OUT,))
-    p.t("ql_nope", (d.NH, d.D_C))
-    p.t("q_pe", (d.NH, d.D_R))
+    p.t("x_res", (d.H,), "pk16")
+    p.t("x_mid", (d.H,), "pk16")
+    p.t("qkva", (d.Q_OUT + d.KVA_OUT,), "pk16")
+    p.t("ql_nope", (d.NH, d.D_C), "pk16")
+    p.t("q_pe", (d.NH, d.D_R), "pk16")
+    p.t("crow", (XCDS, d.D_C + d.D_R), "pk16")
     p.t("partials", (n_splits, d.NH, partials_row(d.D_C)), "f32")
+    p.t("att_done", (XCDS, XWORKERS), "pk32")
     p.t("o_merged", (d.NH, d.D_C))
-    p.t("attn", (d.NH * d.D_V,))
+    p.t("attn", (d.NH * d.D_V,), "pk16")
     p.t("cos", (s_max, d.D_R), kind="input", source="capture:cos")
     p.t("sin", (s_max, d.D_R), kind="input", source="capture:sin")
-    p.t("amax", (2 * WORKERS,), "f32")
+    p.t("amax", (2 * WORKERS,), "pk32")
     if layers >= 1:
-        p.t("act", (d.I_DENSE,))
+        p.t("act", (d.I_DENSE,), "pk16")
         p.t("h", (d.H,))
     if layers >= 2:
-        p.t("logits_x", (XCDS, d.E), "f32")
+        p.t("logits_x", (d.E,), "pk32")
         p.t("topk_w", (TOPK_TOTAL_SLOTS,), "f32")
         p.t("routing", (d.E_TOTAL,), "i32")
         p.t("mask", (d.E_TOTAL + 1,), "i32")
         p.t("logits_router", (d.E,), "f32")
         p.t("sel", (XCDS,), "i32")
-        p.t("act8", (TOPK_TOTAL_SLOTS, d.I_MOE))
+        p.t("act8", (TOPK_TOTAL_SLOTS, d.I_MOE), "pk16")
         p.t("out8", (TOPK_TOTAL_SLOTS, d.H))
         p.t("route_log", (iters_cap, d.L - 1, TOPK_TOTAL_SLOTS), "i32")
-    if debug_scores:
-        p.t("scores", (d.NH, s_max), "f32")
 
-    p.op("embed_layer", 1, NONE, "prologue.embed", "folded into L0.qkva's input prologue",
+    p.op("embed_layer", 1, "prologue.embed", "folded into L0.qkva's input prologue",
          input="tokens", weight="W_embed", output="x_res", amax="amax" if head else None)
     for l in range(layers):
         p.t(f"w_norm1_{l}", (d.H,), kind="input", source=f"w_norm1_{l}")
@@ -193,46 +195,45 @@ def build_plan(dims: Dims = REAL_DIMS, s_max: int = 1056, layers: int = 27, head
         p.t(f"W_o_{l}", (d.H, d.NH * d.D_V), kind="input", source=f"W_o_{l}")
         p.t(f"c_kv_{l}", (s_max, d.D_C), kind="input", source=f"capture:c_kv_{l}")
         p.t(f"k_pe_{l}", (s_max, d.D_R), kind="input", source=f"capture:k_pe_{l}")
-        p.op("linear_gemv_layer", WORKERS, GLOBAL, f"L{l}.qkva", input="x_res", w_norm=f"w_norm1_{l}",
+        p.op("linear_gemv_layer", WORKERS, f"L{l}.qkva", input="x_res", w_norm=f"w_norm1_{l}",
              weight=f"W_qkva_{l}", residual=None, output="qkva", norm=True)
-        p.op("mla_prep_layer", XCDS * (2 * d.D_C // 128 + 1), XCD, f"L{l}.mla_prep", qkva="qkva",
+        p.op("mla_prep_layer", XCDS * (2 * d.D_C // 32 + 1), f"L{l}.mla_prep", qkva="qkva",
              w_kv_norm=f"w_kv_norm_{l}", w_uk=f"W_uk_{l}", cos="cos", sin="sin", c_kv=f"c_kv_{l}",
-             k_pe=f"k_pe_{l}", ql_nope="ql_nope", q_pe="q_pe")
-        p.op("mla_attend_layer", XCDS * n_splits, XCD, f"L{l}.mla_attend", ql_nope="ql_nope", q_pe="q_pe",
-             c_kv=f"c_kv_{l}", k_pe=f"k_pe_{l}", partials="partials", o_merged="o_merged",
-             scores="scores" if debug_scores else None, softmax_scale=softmax_scale, split=split, n_splits=n_splits)
-        p.op("mla_merge_uv_layer", WORKERS, GLOBAL, f"L{l}.mla_merge_uv", input="o_merged", w_uv=f"W_uv_{l}",
-             output="attn")
-        p.op("linear_gemv_layer", WORKERS, GLOBAL, f"L{l}.o_proj", input="attn", w_norm=None, weight=f"W_o_{l}",
-             residual="x_res", output="x_res", norm=False)
+             k_pe=f"k_pe_{l}", ql_nope="ql_nope", q_pe="q_pe", crow="crow")
+        p.op("mla_attend_layer", XCDS * n_splits, f"L{l}.mla_attend", ql_nope="ql_nope", q_pe="q_pe", crow="crow",
+             c_kv=f"c_kv_{l}", k_pe=f"k_pe_{l}", partials="partials", done="att_done",
+             softmax_scale=softmax_scale, split=split, n_splits=n_splits)
+        p.op("mla_merge_uv_layer", WORKERS, f"L{l}.mla_merge_uv", input="partials", done="att_done",
+             w_uv=f"W_uv_{l}", output="attn", o_merged="o_merged", split=split, n_splits=n_splits)
+        p.op("linear_gemv_layer", WORKERS, f"L{l}.o_proj", input="attn", w_norm=None, weight=f"W_o_{l}",
+             residual="x_res", output="x_mid", norm=False)
         if l == 0:
             p.t("W_gu_0", (2 * d.I_DENSE, d.H), kind="input", source="W_gu_0")
             p.t("W_down_0", (d.H, d.I_DENSE), kind="input", source="W_down_0")
-            p.op("gang_linear_silu_layer", WORKERS, GLOBAL, f"L{l}.gate_up", input="x_res", w_norm=f"w_norm2_{l}",
+            p.op("gang_linear_silu_layer", WORKERS, f"L{l}.gate_up", input="x_mid", w_norm=f"w_norm2_{l}",
                  weight="W_gu_0", output="act", h="h")
-            p.op("linear_gemv_layer", WORKERS, GLOBAL, f"L{l}.down", input="act", w_norm=None, weight="W_down_0",
-                 residual="x_res", output="x_res", norm=False)
+            p.op("linear_gemv_layer", WORKERS, f"L{l}.down", input="act", w_norm=None, weight="W_down_0",
+                 residual="x_mid", output="x_res", norm=False)
         else:
             p.t(f"W_gate_{l}", (d.E, d.H), kind="input", source=f"W_gate_{l}")
             p.t(f"W13_{l}", (d.E_TOTAL, 2 * d.I_MOE, d.H), kind="input", source=f"W13_{l}")
             p.t(f"W2_{l}", (d.E_TOTAL, d.H, d.I_MOE), kind="input", source=f"W2_{l}")
-            p.op("moe_router_layer", d.TOPK * (WORKERS // XCDS), XCD, f"L{l}.router", input="x_res",
-                 w_norm=f"w_norm2_{l}", w_gate=f"W_gate_{l}", logits_x="logits_x")
-            p.op("gang_moe_w13_gemv_layer", WORKERS, XCD, f"L{l}.w13", input="x_res", w_norm=f"w_norm2_{l}",
+            p.op("moe_router_layer", d.E, f"L{l}.router", input="x_mid", w_norm=f"w_norm2_{l}",
+                 w_gate=f"W_gate_{l}", logits_x="logits_x")
+            p.op("gang_moe_w13_gemv_layer", WORKERS, f"L{l}.w13", input="x_mid", w_norm=f"w_norm2_{l}",
                  logits_x="logits_x", weight=f"W13_{l}", output="act8", topk_w="topk_w", routing="routing",
                  mask="mask", logits="logits_router", route_log="route_log", h="h", sel="sel", layer_index=l - 1)
-            p.op("gang_moe_w2_linear_layer", WORKERS, GLOBAL, f"L{l}.w2", input="act8", sel="sel", weight=f"W2_{l}",
-                 output="out8")
-            p.op("moe_mul_sum_add_layer", WORKERS, GLOBAL, f"L{l}.combine",
-                 "folded into the next GEMV's input prologue when one follows",
-                 input="out8", weight="topk_w", residual="x_res", output="x_res")
+            p.op("gang_moe_w2_linear_layer", WORKERS, f"L{l}.w2", input="act8", logits_x="logits_x",
+                 weight=f"W2_{l}", output="out8")
+            p.op("moe_mul_sum_add_layer", WORKERS, f"L{l}.combine", "folded into the w2 stage (8 rows per worker, all slots)",
+                 input="out8", weight="topk_w", residual="x_mid", output="x_res")
     if head:
         p.t("w_final_norm", (d.H,), kind="input", source="w_final_norm")
         p.t("W_lm", (d.V, d.H), kind="input", source="W_lm")
         p.t("logits", (d.V,))
-        p.op("linear_gemv_layer", WORKERS, GLOBAL, "head.lm_head", input="x_res", w_norm="w_final_norm",
+        p.op("linear_gemv_layer", WORKERS, "head.lm_head", input="x_res", w_norm="w_final_norm",
              weight="W_lm", residual=None, output="logits", amax="amax", norm=True)
-        p.op("argmax_reduce_layer", 1, GLOBAL, "head.argmax_reduce",
+        p.op("argmax_reduce_layer", 1, "head.argmax_reduce",
              "folded into the next iteration's embed; the last iteration's runs as the epilogue",
              input="amax", output="tokens")
     return p
@@ -240,5 +241,4 @@ def build_plan(dims: Dims = REAL_DIMS, s_max: int = 1056, layers: int = 27, head
 
 def summary(p: Plan) -> dict:
     return {"ops": p.n_ops, "tasks": p.n_tasks, "n_splits": p.n_splits, "split": p.split,
-            "syncs_global": sum(c.sync == GLOBAL for c in p.calls),
-            "syncs_xcd": sum(c.sync == XCD for c in p.calls)}
+            "packet_tensors": sum(t.dtype in ("pk16", "pk32") for t in p.tensors.values())}

@@ -18,14 +18,13 @@ PKG = Path(__file__).resolve().parent.parent
 LIB_PATH = Path(os.environ.get("FX_LIB", PKG / "lib" / "libfleet_mi355x.so"))
 
 FX_OP_GEMV, FX_OP_MLA_PREP, FX_OP_MLA_ATTEND, FX_OP_MLA_MERGE_UV = 1, 2, 3, 4
-FX_OP_MOE_ROUTER, FX_OP_MOE_W13, FX_OP_MOE_W2, FX_OP_MOE_COMBINE = 5, 6, 7, 8
+FX_OP_MOE_ROUTER, FX_OP_MOE_W13, FX_OP_MOE_W2 = 5, 6, 7
 FX_OP_DENSE_GU, FX_OP_ARGMAX = 9, 10
-FX_IN_VEC, FX_IN_EMBED, FX_IN_COMBINE = 0, 1, 2
-FX_F_NORM, FX_F_RESIDUAL, FX_F_WRITE_X, FX_F_ARGMAX, FX_F_HEAD = 1, 2, 4, 8, 16
-FX_SYNC_NONE, FX_SYNC_XCD, FX_SYNC_GLOBAL = 0, 1, 2
-FX_MAX_ITERS, FX_MAX_MARKS = 65536, 256
-FX_ABI_VERSION = 2
-WORKERS = 248          # 256 CUs minus one scheduler workgroup per XCD
+FX_IN_VEC, FX_IN_EMBED = 0, 1
+FX_F_NORM, FX_F_RESIDUAL, FX_F_ARGMAX, FX_F_HEAD, FX_F_OUT_LL, FX_F_RES_EMBED = 1, 2, 8, 16, 32, 64
+FX_MAX_ITERS, FX_MAX_MARKS, FX_PROF_SLOTS = 65536, 256, 4
+FX_ABI_VERSION = 3
+WORKERS = 256          # one worker workgroup per CU
 XCDS = 8
 
 
@@ -36,8 +35,8 @@ class FxError(RuntimeError):
 class FxStage(ctypes.Structure):
     """Mirror of struct fx_stage (include/fleet_mi355x.h)."""
     _fields_ = [(n, ctypes.c_int32) for n in (
-        "op", "sync", "flags", "in_kind", "layer", "n_rows", "k", "n_slots", "topk", "n_forced", "split", "n_splits",
-        "d_c", "d_r", "d_n", "prow", "s_scores", "s_max", "aux_i0", "aux_i1")] + \
+        "op", "flags", "in_kind", "layer", "n_rows", "k", "n_slots", "topk", "n_forced", "split", "n_splits",
+        "d_c", "d_r", "d_n", "prow", "s_max", "aux_i0", "aux_i1")] + [("src", ctypes.c_int32 * 4)] + \
         [(n, ctypes.c_float) for n in ("eps", "scale", "scaling", "aux_f")] + \
         [(n, ctypes.c_uint64) for n in ("w", "x", "w_norm", "res", "out")] + [("aux", ctypes.c_uint64 * 8)]
 
@@ -46,17 +45,21 @@ class FxStage(ctypes.Structure):
             if k == "aux":
                 for i, p in v.items():
                     self.aux[i] = int(p or 0)
+            elif k == "src":
+                for i, p in enumerate(v):
+                    self.src[i] = int(p)
             else:
                 setattr(self, k, v if not isinstance(v, DeviceBuffer) else v.ptr)
         return self
 
     def to_dict(self):
-        d = {n: getattr(self, n) for n, _ in self._fields_ if n != "aux"}
+        d = {n: getattr(self, n) for n, _ in self._fields_ if n not in ("aux", "src")}
         d["aux"] = list(self.aux)
+        d["src"] = list(self.src)
         return d
 
 
-assert ctypes.sizeof(FxStage) == 200, ctypes.sizeof(FxStage)   # static_assert in fx_runtime.hip
+assert ctypes.sizeof(FxStage) == 208, ctypes.sizeof(FxStage)   # static_assert in fx_runtime.hip
 
 _lib = None
 
@@ -94,7 +97,7 @@ def lib():
         "fx_last_run_ms": (ctypes.c_int, [vp, ctypes.POINTER(ctypes.c_float)]),
         "fx_set_profile": (ctypes.c_int, [vp, i32]),
         "fx_read_profile": (ctypes.c_int, [vp, ctypes.POINTER(ctypes.c_uint64), i32]),
-        "fx_run_stage": (ctypes.c_int, [vp, ctypes.POINTER(FxStage), i32, i32, vp]),
+        "fx_run_stage": (ctypes.c_int, [vp, ctypes.POINTER(FxStage), i32, ctypes.c_uint32, i32, vp]),
         "fx_gen_normal_bf16": (ctypes.c_int, [vp, vp, u64, u64, u64, u64, u64, u64, ctypes.c_uint32, ctypes.c_float]),
         "fx_fill_u16": (ctypes.c_int, [vp, vp, u64, ctypes.c_uint16]),
     }
@@ -191,21 +194,23 @@ class Runtime:
         self.check(self.L.fx_set_profile(self.h, iteration), "fx_set_profile")
 
     def read_profile(self, n_stages):
-        """[n_stages, 256, 2] s_memrealtime stamps (100 MHz) of the profiled iteration."""
-        n = n_stages * 256 * 2
+        """[n_stages, 256, FX_PROF_SLOTS] s_memrealtime stamps (100 MHz) of the profiled iteration."""
+        n = n_stages * 256 * FX_PROF_SLOTS
         buf = (ctypes.c_uint64 * n)()
         m = self.L.fx_read_profile(self.h, buf, n)
         if m != n:
             raise FxError(f"fx_read_profile returned {m} of {n}")
-        return np.array(buf, np.uint64).reshape(n_stages, 256, 2)
+        return np.array(buf, np.uint64).reshape(n_stages, 256, FX_PROF_SLOTS)
 
     def timing(self, n):
         buf = (ctypes.c_uint64 * (n + 1))()
         m = self.L.fx_read_timing(self.h, buf, n + 1)
         return np.array(buf[:max(m, 0)], np.uint64)
 
-    def run_stage(self, stage, step=0, it=0):
-        self.check(self.L.fx_run_stage(self.h, ctypes.byref(stage), step, it, None), "fx_run_stage")
+    def run_stage(self, stage, step=0, tbase=1000, sidx=5):
+        """One stage as a standalone launch: packet inputs must carry tbase + src[k] + 1, outputs get
+        tbase + sidx + 1."""
+        self.check(self.L.fx_run_stage(self.h, ctypes.byref(stage), step, tbase, sidx, None), "fx_run_stage")
 
     def close(self):
         if self.h:
@@ -219,7 +224,8 @@ class Runtime:
             pass
 
 
-_DT = {"bf16": np.uint16, "f32": np.float32, "i32": np.int32, "i64": np.int64, "u16": np.uint16, "u8": np.uint8}
+_DT = {"bf16": np.uint16, "f32": np.float32, "i32": np.int32, "i64": np.int64, "u16": np.uint16, "u8": np.uint8,
+       "u64": np.uint64, "pk16": np.uint64, "pk32": np.uint64}
 
 
 class DeviceBuffer:
@@ -230,12 +236,18 @@ class DeviceBuffer:
         self.shape = tuple(int(s) for s in (shape if isinstance(shape, (tuple, list)) else (shape,)))
         self.dtype = dtype
         self.np_dtype = _DT[dtype]
-        self.nbytes = int(np.prod(self.shape, dtype=np.int64)) * np.dtype(self.np_dtype).itemsize
+        n = int(np.prod(self.shape, dtype=np.int64))
+        if dtype == "pk16":         # bf16 values as packets: 2 values + tag per 8 bytes
+            assert n % 4 == 0, (shape, "packet vectors hold a multiple of 4 bf16 values")
+            n //= 2
+        self.n_words = n
+        self.nbytes = n * np.dtype(self.np_dtype).itemsize
         p = ctypes.c_void_p()
         rt.check(rt.L.fx_malloc(rt.h, max(self.nbytes, 16), ctypes.byref(p)), "fx_malloc")
         self.ptr = p.value
 
     def upload(self, arr):
+        assert self.dtype not in ("pk16", "pk32"), "packet buffers: upload_packets"
         a = np.ascontiguousarray(arr, dtype=self.np_dtype)
         assert a.nbytes == self.nbytes, (a.shape, self.shape)
         self.rt.check(self.rt.L.fx_memcpy_htod(self.rt.h, self.ptr, a.ctypes.data, a.nbytes), "htod")
@@ -247,10 +259,33 @@ class DeviceBuffer:
         assert elem_offset * it + a.nbytes <= self.nbytes
         self.rt.check(self.rt.L.fx_memcpy_htod(self.rt.h, self.ptr + elem_offset * it, a.ctypes.data, a.nbytes), "htod")
 
-    def download(self):
-        out = np.empty(self.shape, self.np_dtype)
+    def download_raw(self):
+        out = np.empty(self.n_words, self.np_dtype)
         self.rt.check(self.rt.L.fx_memcpy_dtoh(self.rt.h, out.ctypes.data, self.ptr, self.nbytes), "dtoh")
         return out
+
+    def download(self, tag=None):
+        """The values (packets unpacked: bf16 bits as uint16, f32 as float32); with `tag`, every packet
+        must carry it."""
+        raw = self.download_raw()
+        if self.dtype in ("pk16", "pk32"):
+            vals, tags = unpack_packets(raw, self.dtype)
+            if tag is not None and not (tags == np.uint32(tag)).all():
+                bad = np.flatnonzero(tags != np.uint32(tag))
+                raise FxError(f"packet tags differ from {tag} at {bad[:8].tolist()} ({len(bad)} packets): {tags[bad[:8]].tolist()}")
+            return vals.reshape(self.shape)
+        return raw.reshape(self.shape)
+
+    def upload_packets(self, values, tag):
+        """Write `values` (bf16 bits for pk16, float32 for pk32) as packets carrying `tag`."""
+        self.upload_raw(pack_packets(values, self.dtype, tag))
+        return self
+
+    def upload_raw(self, arr):
+        a = np.ascontiguousarray(arr, dtype=self.np_dtype).reshape(-1)
+        assert a.nbytes == self.nbytes, (a.shape, self.shape)
+        self.rt.check(self.rt.L.fx_memcpy_htod(self.rt.h, self.ptr, a.ctypes.data, a.nbytes), "htod")
+        return self
 
     def download_range(self, elem_offset, n):
         it = np.dtype(self.np_dtype).itemsize
@@ -273,3 +308,28 @@ class DeviceBuffer:
                 self.free()
         except Exception:
             pass
+
+
+def pack_packets(values, dtype, tag):
+    """Packet words (uint64) of a value vector: pk16 = two bf16 (uint16 bits, element 2i low) per
+    packet, pk32 = one float32 per packet; the tag in the high 32 bits."""
+    v = np.ascontiguousarray(values).reshape(-1)
+    if dtype == "pk16":
+        u = v.astype(np.uint16).astype(np.uint64)
+        payload = u[0::2] | (u[1::2] << np.uint64(16))
+    else:
+        payload = np.ascontiguousarray(v, np.float32).view(np.uint32).astype(np.uint64)
+    return payload | (np.uint64(tag & 0xFFFFFFFF) << np.uint64(32))
+
+
+def unpack_packets(words, dtype):
+    """(values, tags) of packet words: values as uint16 bf16 bits (pk16) or float32 (pk32)."""
+    w = np.ascontiguousarray(words, np.uint64)
+    payload = (w & np.uint64(0xFFFFFFFF)).astype(np.uint32)
+    tags = (w >> np.uint64(32)).astype(np.uint32)
+    if dtype == "pk16":
+        vals = np.empty(2 * len(w), np.uint16)
+        vals[0::2] = (payload & np.uint32(0xFFFF)).astype(np.uint16)
+        vals[1::2] = (payload >> np.uint32(16)).astype(np.uint16)
+        return vals, tags
+    return payload.view(np.float32), tags

@@ -1,0 +1,110 @@
+#!/usr/bin/env python3
+"""gfx950 memory-system probes (csrc/fx_probe.hip, lib/libfleet_probe.so): the stream rate of the
+GEMV load pattern against bytes per workgroup and loads in flight, dependent-load latency per cache
+policy (idle and under a full-chip stream), and the flag round trip between two workgroups.
+The reference's env/hw/probes (stream_read.cu, chase.cu, fence_probe.cu) measured the same on
+MI300X; the decode kernel's prefetch depth and synchronisation design follow these numbers.
+
+    python fleet-amd-task_amd/harness/probes.py [--out probes.md]
+"""
+import argparse
+import ctypes
+import sys
+from pathlib import Path
+
+import numpy as np
+
+PKG = Path(__file__).resolve().parent.parent
+sys.path.insert(0, str(PKG))
+from fleet import runtime as R  # noqa: E402
+
+TICK_NS = 10.0   # s_memrealtime: 100 MHz
+
+
+def probe_lib():
+    p = PKG / "lib" / "libfleet_probe.so"
+    if not p.exists():
+        raise R.FxError(f"{p} is missing: make -C fleet-amd-task_amd/csrc probe")
+    L = ctypes.CDLL(str(p))
+    vp, u64, u32 = ctypes.c_void_p, ctypes.c_uint64, ctypes.c_uint32
+    L.fxp_stream.argtypes = [vp, u64, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.POINTER(u64),
+                             ctypes.POINTER(ctypes.c_float)]
+    L.fxp_chase.argtypes = [vp, u32, ctypes.c_int, vp, u64, ctypes.c_int, ctypes.POINTER(u64)]
+    L.fxp_pingpong.argtypes = [ctypes.c_int, ctypes.c_int, u32, vp, u64, ctypes.c_int, ctypes.POINTER(u64)]
+    return L
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--out", default=None)
+    args = ap.parse_args()
+    rt = R.Runtime(0)
+    L = probe_lib()
+    lines = []
+
+    def say(s):
+        print(s, flush=True)
+        lines.append(s)
+
+    big = rt.alloc((2 << 30,), "u8")
+    rt.fill_u16(big, 0x3F80, n=big.nbytes // 2)
+    rt.synchronize()
+    # ---- stream
+    say("## stream: 256 workgroups, GEMV load pattern (each wave: `depth` x 1 KiB loads in flight)\n")
+    say("| threads | depth | KiB/workgroup | GB/s (events) | median µs/wg | max µs/wg |")
+    say("|---|---|---|---|---|---|")
+    ticks = (ctypes.c_uint64 * 256)()
+    ms = ctypes.c_float()
+    for threads in (256, 512):
+        for depth in (4, 8, 16, 32):
+            for kib in (16, 64, 256, 1024, 4096):
+                if threads == 512 and depth == 32:
+                    continue
+                by = kib * 1024
+                for rep in range(2):
+                    rc = L.fxp_stream(ctypes.c_void_p(big.ptr), by, 256, threads, depth, ticks, ctypes.byref(ms))
+                    assert rc == 0, rc
+                t = np.array(ticks, np.float64) * TICK_NS / 1e3
+                say(f"| {threads} | {depth} | {kib} | {256 * by / (ms.value * 1e-3) / 1e9:.0f} | {np.median(t):.2f} | {t.max():.2f} |")
+    # ---- chase
+    say("\n## dependent-load latency (one lane, pointer chase, stride 256 B)\n")
+    say("| footprint | policy | load | ns/load |")
+    say("|---|---|---|---|")
+    rng = np.random.default_rng(1)
+    for slots, name in ((4096, "1 MiB"), (2 << 20, "512 MiB")):
+        stride = 64
+        perm = rng.permutation(slots).astype(np.uint32)
+        nxt = np.zeros(slots * stride, np.uint32)
+        # a single cycle through the permutation
+        order = perm
+        nxt[order[:-1] * stride] = order[1:] * stride
+        nxt[order[-1] * stride] = order[0] * stride
+        buf = rt.alloc((slots * stride,), "i32")
+        buf.upload(nxt.view(np.int32))
+        out = (ctypes.c_uint64 * 3)()
+        hops = 2000
+        for mode, pol in ((0, "plain"), (1, "sc1"), (2, "nt")):
+            for load in (False, True):
+                lp = ctypes.c_void_p(big.ptr) if load else None
+                rc = L.fxp_chase(ctypes.c_void_p(buf.ptr), hops, mode, lp, big.nbytes, 256, out)
+                assert rc == 0, rc
+                say(f"| {name} | {pol} | {'stream' if load else 'idle'} | {out[0] * TICK_NS / hops:.0f} |")
+        buf.free()
+    # ---- ping-pong
+    say("\n## flag round trip between two workgroups (agent-scope relaxed store / load)\n")
+    say("| a (XCD) | b (XCD) | load | ns/round trip |")
+    say("|---|---|---|---|")
+    out = (ctypes.c_uint64 * 3)()
+    for a, b in ((8, 16), (8, 9), (8, 13)):
+        for load in (False, True):
+            lp = ctypes.c_void_p(big.ptr) if load else None
+            rc = L.fxp_pingpong(a, b, 2000, lp, big.nbytes, 256, out)
+            assert rc == 0 and out[1] == 1, (rc, out[1])
+            say(f"| {a} ({a % 8}) | {b} ({b % 8}) | {'stream' if load else 'idle'} | {out[0] * TICK_NS / 2000:.0f} |")
+    if args.out:
+        Path(args.out).write_text("\n".join(lines) + "\n")
+    rt.close()
+
+
+if __name__ == "__main__":
+    main()

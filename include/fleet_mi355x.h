@@ -8,7 +8,7 @@
  * This header is that boundary as a C ABI: plain pointers and sizes, no torch types. The host
  * (fleet/build_graph.py's counterpart, through ctypes) owns every device buffer of the model and
  * hands raw device pointers in a task table (the plan's calls, one fx_stage each); the library
- * owns only its synchronisation flags and timing slots.
+ * owns only its error flag and timing slots.
  *
  * Errors: every entry returns 0 on success or a nonzero FX_E_* code; fx_last_error() returns the
  * message of the last failure on that context (mirrors the suite's exit codes,
@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define FX_ABI_VERSION 2
+#define FX_ABI_VERSION 3
 
 /* ---- error codes ---------------------------------------------------------------------------- */
 #define FX_OK 0
@@ -35,79 +35,91 @@ extern "C" {
 #define FX_E_DEVICE 3      /* the device is not a gfx950 with the expected layout */
 #define FX_E_STATE 4       /* call out of order (no plan loaded, ...) */
 
+/* ---- dataflow between stages ------------------------------------------------------------------
+ * There is no barrier between stages. Every activation one stage hands to another travels as
+ * tagged packets: 8 bytes = a 32-bit payload (two bf16, element 2i in the low half, or one f32)
+ * and the 32-bit tag of the producing stage. A consumer polls exactly the packets it needs until
+ * their tags equal the producer's tag, so a stage starts as soon as its own inputs exist (and
+ * issues its weight loads before it polls). Tags: stage s of iteration i of a launch with
+ * epoch0 E writes tag E + i * n_stages + s + 1; fx_stage.src[k] names the stage (index in the
+ * table, negative = that many stages back, i.e. the previous iteration) whose tag input k
+ * carries. Buffers marked "packets" below hold 8 bytes per value pair (bf16) or per value (f32)
+ * and must be zeroed before first use (tag 0 is never produced). Plain buffers (caches, partials,
+ * dumps) are ordinary arrays. */
+
 /* ---- operators of the task table --------------------------------------------------------------
- * One per plan call (fleet/graph_plan.py OUTPUT_ARGS names in brackets). Pointer fields of
- * fx_stage used by each op are listed with it; every device pointer is a bf16 (uint16) array
- * unless marked f32 / i32 / i64. */
+ * One per plan call (fleet/graph_plan.py OUTPUT_ARGS names in brackets). Every device pointer is
+ * a bf16 (uint16) array unless marked f32 / i32 / i64 / packets. 256 workers: worker w is workgroup
+ * w, on XCD w % 8, rank w / 8 of its XCD's 32. */
 enum fx_op {
-  /* [linear_gemv_layer] out[n] = bf16(dot(w[n], xin) (+ res[n])) for n < n_rows; K = k.
-   * Input xin by in_kind: FX_IN_VEC x; FX_IN_EMBED w_embed(aux0)[token]; FX_IN_COMBINE
-   * bf16(x + sum_s out8(aux0)[s] * topk_w(aux1 f32)[s]). FX_F_NORM: xin := rmsnorm(xin, w_norm).
-   * FX_F_WRITE_X: worker 0 also stores the prologue's row (before the norm) to x_out(aux2).
-   * FX_F_ARGMAX: per-worker (max, index) of the bf16 outputs to amax(aux3 f32[2*workers]).
-   * FX_IN_EMBED reads the token from tokens(aux4 i64)[step] or, at or past n_prompt, reduces
-   * the previous head's amax(aux3) and stores the id to tokens[step]. */
+  /* [linear_gemv_layer] out[n] = bf16(dot(w[n], xin) (+ res[n])) for n < n_rows; K = k; rows in
+   * groups of 4 split over all workers. Input xin by in_kind: FX_IN_VEC x (packets, src[0]);
+   * FX_IN_EMBED w_embed(aux0)[token], token = tokens(aux4 i64)[step] inside the prompt, else the
+   * argmax of amax(aux3 packets f32, src[1]), stored by worker 0 to tokens[step].
+   * FX_F_NORM: xin := rmsnorm(xin, w_norm). FX_F_RESIDUAL: res (packets, src[2]);
+   * FX_F_RES_EMBED: the residual is w_embed(aux0)[token of this iteration].
+   * FX_F_OUT_LL: out is packets, else a plain bf16 array. FX_F_ARGMAX: per-worker (max, index) of
+   * the bf16 outputs to amax(aux3 packets f32 [2 * 256]). */
   FX_OP_GEMV = 1,
-  /* [mla_prep_layer] qkva(x) -> c_kv(aux0)[step], k_pe(aux1)[step] (cache rows), ql_nope(out)
-   * [nh, d_c], q_pe(aux2) [nh, d_r]; w = W_uk [nh, d_n, d_c]; w_norm = kv_a_layernorm weight;
-   * cos(aux3), sin(aux4) [s_max, d_r]. Heads nh/8 per XCD. */
+  /* [mla_prep_layer] qkva(x packets, src[0]) -> cache rows c_kv(aux0)[step], k_pe(aux1)[step]
+   * (plain), ql_nope(out packets) [nh, d_c], q_pe(aux2 packets) [nh, d_r], and per XCD a packet copy
+   * of the cache row crow(aux5 packets) [8][d_c + d_r]; w = W_uk [nh, d_n, d_c]; w_norm =
+   * kv_a_layernorm weight; cos(aux3), sin(aux4) [s_max, d_r]. XCD x owns heads 2x, 2x + 1. */
   FX_OP_MLA_PREP = 2,
-  /* [mla_attend_layer] ql_nope(x), q_pe(aux2), c_kv(aux0), k_pe(aux1) -> partials(out f32)
-   * [n_splits, nh, prow]; optional scores(aux3 f32) [nh, s_scores]; the last split task of each
-   * XCD merges its heads' live splits into o_merged(aux4) [nh, d_c] (bf16). */
+  /* [mla_attend_layer] ql_nope(x packets), q_pe(aux2 packets), crow(aux5 packets) (src[0] each),
+   * caches c_kv(aux0), k_pe(aux1) -> partials(out f32) [n_splits, nh, prow] (o, then lse at d_c) for
+   * the live splits, split j on rank j % 32 of each XCD; each worker then publishes a done packet
+   * done(aux6 packets f32) [8][32]. */
   FX_OP_MLA_ATTEND = 3,
-  /* [mla_merge_uv_layer] attn(out)[h*d_v+v] = bf16(dot(o_merged(x)[h], W_uv(w)[h][v])), d_v in
-   * the d_n field; the LSE merge of the partials into o_merged ran at the end of MLA_ATTEND. */
+  /* [mla_merge_uv_layer] the LSE merge of head h's live partials (x f32, after done(aux6), src[0])
+   * into bf16 o, then attn(out packets)[h*d_v+v] = bf16(dot(o, W_uv(w)[h][v])), d_v in the d_n field;
+   * ranks 0..15 / 16..31 of XCD x take heads 2x / 2x + 1, 8 rows each; o to o_merged(aux4) (plain). */
   FX_OP_MLA_MERGE_UV = 4,
-  /* [moe_router_layer] h = rmsnorm(x_res(x), w_norm); logits_x(out f32)[xcd][e] = dot(W_gate(w)[e], h)
-   * computed by every XCD for its own use (XCDs whose slot is a forced expert skip it). */
+  /* [moe_router_layer] h = rmsnorm(x_res(x packets, src[0]), w_norm); logits(out packets f32)[e] =
+   * dot(W_gate(w)[e], h) for e < n_rows, row e on worker e. */
   FX_OP_MOE_ROUTER = 5,
-  /* [gang_moe_w13_gemv_layer] softmax/top-k of logits_x(aux0 f32)[xcd], slot xcd's expert e;
-   * act8(out)[slot][i] = bf16(silu(bf16(W13(w)[e][i] h)) * bf16(W13[e][I+i] h)), h recomputed
-   * from x_res(x) and w_norm. Worker 0 of XCD 0 stores topk_w(aux1 f32), routing(aux2 i32),
-   * mask(aux3 i32), logits(aux4 f32), h(aux6) and route_log(aux5 i32 [prow][aux_i1][n_slots]) at
-   * row step - (n_prompt - 1) when that row is in [0, prow); rank 0 of each XCD stores its slot's
-   * expert id to sel(aux7 i32 [8]); aux_i0 = E. */
+  /* [gang_moe_w13_gemv_layer] softmax/top-k of logits(aux0 packets f32, src[0]); slot x on XCD x
+   * (top-k routed, then the n_forced shared experts E, E+1); h = rmsnorm(x_res(x packets, src[1]));
+   * act8(out packets)[slot][i] = bf16(silu(bf16(W13(w)[e][i] h)) * bf16(W13[e][I+i] h)), I = n_rows.
+   * Worker 0 stores topk_w(aux1 f32), routing(aux2 i32), mask(aux3 i32), logits(aux4 f32), h(aux6)
+   * and route_log(aux5 i32 [prow][aux_i1][n_slots]) at row step - (n_prompt - 1) when that row is in
+   * [0, prow); rank 0 of each XCD stores its slot's expert id to sel(aux7 i32 [8]); aux_i0 = E. */
   FX_OP_MOE_W13 = 6,
-  /* [gang_moe_w2_linear_layer] out8(out)[slot][n] = bf16(dot(W2(w)[e][n], act8(x)[slot])),
-   * e = sel(aux7)[slot]. */
+  /* [gang_moe_w2_linear_layer + moe_mul_sum_add_layer] out8[s][n] = bf16(dot(W2(w)[e_s][n],
+   * act8(x packets, src[0])[s])) for every slot s, experts from logits(aux0 packets f32, src[1]);
+   * x_new(out packets)[n] = bf16(x_res(res packets, src[2])[n] + sum_s out8[s][n] * topk_w[s])
+   * (slot order); n_rows = H rows in groups of 8 per worker, k = I; out8 also to aux1 when non-NULL. */
   FX_OP_MOE_W2 = 7,
-  /* [moe_mul_sum_add_layer] x_res(out) = bf16(x_res(x) + sum_s out8(aux0)[s] * topk_w(aux1 f32)[s]). */
-  FX_OP_MOE_COMBINE = 8,
-  /* [gang_linear_silu_layer] h = rmsnorm(x_res(x), w_norm); act(out)[i] = bf16(silu(bf16(w[i] h)) *
-   * bf16(w[I+i] h)) for i < n_rows (= I); h to aux6 when non-NULL. */
+  /* [gang_linear_silu_layer] h = rmsnorm(x_res(x packets, src[0]), w_norm); act(out packets)[i] =
+   * bf16(silu(bf16(w[i] h)) * bf16(w[I+i] h)) for i < n_rows (= I); h to aux6 when non-NULL. */
   FX_OP_DENSE_GU = 9,
-  /* [argmax_reduce_layer] tokens(aux4 i64)[step + 1] = argmax from amax(aux3). */
+  /* [argmax_reduce_layer] tokens(aux4 i64)[step + 1] = argmax from amax(aux3 packets f32, src[0]). */
   FX_OP_ARGMAX = 10,
 };
 
 /* GEMV input kinds */
 #define FX_IN_VEC 0
 #define FX_IN_EMBED 1
-#define FX_IN_COMBINE 2
 
 /* flags */
 #define FX_F_NORM 1u
 #define FX_F_RESIDUAL 2u
-#define FX_F_WRITE_X 4u
 #define FX_F_ARGMAX 8u
 #define FX_F_HEAD 16u      /* the stage belongs to the head: skipped while step + 1 < n_prompt */
-
-/* synchronisation after a stage */
-#define FX_SYNC_NONE 0
-#define FX_SYNC_XCD 1      /* the 31 workers of each XCD, through that XCD's scheduler */
-#define FX_SYNC_GLOBAL 2   /* every worker of the device */
+#define FX_F_OUT_LL 32u    /* output as packets */
+#define FX_F_RES_EMBED 64u /* residual = the embedding row of this iteration's token */
 
 /* One entry of the task table: one operator of the plan (fleet/graph_plan.py Call). */
 typedef struct fx_stage {
-  int32_t op, sync, flags, in_kind;
+  int32_t op, flags, in_kind;
   int32_t layer;      /* decoder layer (route_log row: layer - 1), -1 outside the layers */
-  int32_t n_rows;     /* GEMV/DENSE_GU rows; heads for MLA ops; E for the router */
+  int32_t n_rows;     /* GEMV/DENSE_GU rows; heads for MLA ops; E for the router; H for W2 */
   int32_t k;          /* reduction width (H, or I for W2 / down) */
   int32_t n_slots;    /* MoE slots: topk + forced (8) */
   int32_t topk, n_forced, split, n_splits;
   int32_t d_c, d_r, d_n, prow;
-  int32_t s_scores, s_max, aux_i0, aux_i1;
+  int32_t s_max, aux_i0, aux_i1;
+  int32_t src[4];     /* producing stage of each packet input (see "dataflow") */
   float eps, scale, scaling, aux_f;
   uint64_t w, x, w_norm, res, out;
   uint64_t aux[8];
@@ -117,13 +129,13 @@ typedef struct fx_stage {
 typedef struct fx_ctx fx_ctx;
 
 /* Replaces mi.PersistentKernel(...) (fleet/build_graph.py:583-589): binds a device, checks it is a
- * gfx950 with 8 XCDs, allocates the synchronisation flags. */
+ * gfx950 with 256 CUs in 8 XCDs, allocates the error flag and timing slots. */
 int fx_create(int device, fx_ctx** out);
 int fx_destroy(fx_ctx* ctx);
 const char* fx_last_error(fx_ctx* ctx);
 int fx_abi_version(void);
 
-/* Device facts: CUs, XCDs, workers (CUs minus one scheduler per XCD), LDS per workgroup. */
+/* Device facts: CUs, XCDs, workers (one per CU), LDS per workgroup. */
 int fx_device_info(fx_ctx* ctx, int32_t* cus, int32_t* xcds, int32_t* workers, int32_t* lds_bytes);
 
 /* ---- memory (for hosts without torch: the ctypes runtime allocates through these) ------------- */
@@ -137,7 +149,7 @@ int fx_synchronize(fx_ctx* ctx);
 
 /* ---- plan and run ----------------------------------------------------------------------------- */
 /* Replaces mpk.compile() (the codegen + JIT of the worker switch, harness/run_fleet.py:556): the
- * task table is validated on the host (shapes, pointer presence, sync kinds) and uploaded. */
+ * task table is validated on the host (shapes, pointers, packet sources) and uploaded. */
 int fx_load_plan(fx_ctx* ctx, const fx_stage* stages, int32_t n_stages, const fx_stage* epilogue,
                  int32_t n_epilogue);
 
@@ -152,7 +164,8 @@ int fx_run(fx_ctx* ctx, int32_t iters, int32_t step0, int32_t n_prompt, int64_t*
  * reports a wait that timed out inside any launch since the last fx_finish. fx_run = both. A launch
  * whose iterations all lie inside the prompt (step0 + iters < n_prompt: the head never runs) uses
  * the kernel symbol fx_prefill, every other launch fx_persistent (the same code). iters is at most
- * FX_MAX_ITERS. */
+ * FX_MAX_ITERS. Tags are 32-bit and never reused: a launch that would exhaust them fails with
+ * FX_E_STATE (after about 2^32 / n_stages iterations of one context). */
 #define FX_MAX_ITERS 65536
 int fx_launch(fx_ctx* ctx, int32_t iters, int32_t step0, int32_t n_prompt, int64_t* tokens, void* stream);
 int fx_finish(fx_ctx* ctx, void* stream);
@@ -169,9 +182,11 @@ int fx_marks_ms(fx_ctx* ctx, int32_t i, int32_t j, float* ms);
 
 /* Per-stage event timing of one iteration (the reference's MPK_EVENT_TIMING + measure.py per-op
  * gaps, docs/fleet/03-runtime.md:367-371): when iter >= 0, the next fx_run records for iteration
- * `iter` and every worker two s_memrealtime stamps per stage, [stage][block][start, end], start when
- * the worker begins the stage (after the previous sync), end when its share is done (before the sync).
- * fx_read_profile copies n_stages * 256 * 2 stamps; returns the count written. */
+ * `iter` and every worker FX_PROF_SLOTS s_memrealtime stamps per stage, [stage][worker][slot]:
+ * slot 0 when the worker begins the stage, slot 1 when its packet inputs have arrived, slot 2
+ * when its outputs are issued (0 where a stage has no such point).
+ * fx_read_profile copies n_stages * 256 * FX_PROF_SLOTS stamps; returns the count written. */
+#define FX_PROF_SLOTS 4
 int fx_set_profile(fx_ctx* ctx, int32_t iter);
 int fx_read_profile(fx_ctx* ctx, uint64_t* buf, int32_t n);
 
@@ -181,8 +196,10 @@ int fx_read_profile(fx_ctx* ctx, uint64_t* buf, int32_t n);
 int fx_read_timing(fx_ctx* ctx, uint64_t* buf, int32_t n);
 
 /* Kernel-suite entry (kernel_tests_mi300.cu counterpart): one stage as a standalone launch of all
- * workers, with the same task split as inside fx_run; step is the decode position. */
-int fx_run_stage(fx_ctx* ctx, const fx_stage* stage, int32_t step, int32_t iter, void* stream);
+ * workers, with the same task split as inside fx_run; step is the decode position. Packet inputs
+ * must carry tag tbase + src[k] + 1, outputs get tbase + sidx + 1; the token of an embed residual
+ * is tokens(aux4)[step]. */
+int fx_run_stage(fx_ctx* ctx, const fx_stage* stage, int32_t step, uint32_t tbase, int32_t sidx, void* stream);
 
 /* ---- seeded inputs (pack_weights counterpart: fills the packed keys from a seed) -------------- */
 /* dst[r * dst_stride + j] = bf16(scale * z(src_offset + r * src_stride + j)) for r < rows, j < row_len,

@@ -96,11 +96,12 @@ def test_last_step_buffers_match_oracle(rt):
     tok, routes, x = M.decode_step(cfg, W, oc, cos, sin, token, step, layers, True, rec)
     h = runner.host
     l = layers - 1
+    live = -(-(step + 1) // plan.split)
     checks = {
         "qkva": (h["qkva"].download(), np.concatenate([rec[f"L{l}.B2.q"], rec[f"L{l}.kva"]])),
         "ql_nope": (h["ql_nope"].download(), rec[f"L{l}.ql_nope"]),
         "q_pe": (h["q_pe"].download(), rec[f"L{l}.B4.q_pe"]),
-        "partials": (h["partials"].download()[:, :, :d.D_C + 1], rec[f"L{l}.partials"][:, :, :d.D_C + 1]),
+        "partials": (h["partials"].download()[:live, :, :d.D_C + 1], rec[f"L{l}.partials"][:live, :, :d.D_C + 1]),
         "o_merged": (h["o_merged"].download(), rec[f"L{l}.o_merged"]),
         "attn": (h["attn"].download(), rec[f"L{l}.B6.attn"]),
         "logits_router": (h["logits_router"].download(), rec[f"L{l}.B8.router_logits"]),

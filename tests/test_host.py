@@ -26,11 +26,13 @@ def test_library_exports_every_declared_symbol():
     lib = ctypes.CDLL(str(R.LIB_PATH))
     for name in declared:
         assert hasattr(lib, name), name
-    assert R.lib().fx_abi_version() == R.FX_ABI_VERSION == 2
+    assert R.lib().fx_abi_version() == R.FX_ABI_VERSION == 3
 
 
 def test_stage_struct_size_matches_header():
-    assert ctypes.sizeof(R.FxStage) == 200
+    assert ctypes.sizeof(R.FxStage) == 208
+    # field offsets shared with the C header: src after the 18 int32 fields, pointers 8-aligned
+    assert R.FxStage.src.offset == 72 and R.FxStage.w.offset == 104 and R.FxStage.aux.offset == 144
 
 
 def test_plan_counts_and_chain():
@@ -43,7 +45,7 @@ def test_plan_counts_and_chain():
     t = G.build_plan().truncate("L1.o_proj")
     assert t.calls[-1].label == "L1.o_proj"
     assert G.splits_for(32768, n_splits=32) == (1024, 32)
-    assert G.splits_for(16416, n_splits=128) == (160, 103) or G.splits_for(16416, n_splits=128)[1] <= 128
+    assert G.splits_for(16416, n_splits=128) == (160, 103)
 
 
 class _FakeBuf:
@@ -67,34 +69,44 @@ def _fake_host(plan):
     host = {}
     for name, t in plan.tensors.items():
         host[name] = rt.alloc(t.shape, t.dtype)
-    host["x_res_b"] = rt.alloc((plan.dims.H,), "bf16")
     return host
 
 
 def test_fold_rules():
     p = G.build_plan(layers=3, head=True)
     host = _fake_host(p)
-    stages, epi, xf = B.compile_stages(p, host)
+    stages, epi = B.compile_stages(p, host)
+    labels = B.compile_stages.labels
     ops = [s.op for s in stages]
-    # embed folded into L0.qkva, combines folded into the next GEMV, argmax as the epilogue
+    n = len(stages)
+    # embed folded into L0.qkva, combines folded into their w2, argmax as the epilogue
     assert stages[0].op == R.FX_OP_GEMV and stages[0].in_kind == R.FX_IN_EMBED
-    assert R.FX_OP_MOE_COMBINE not in ops
+    assert not any("combine" in l for l in labels)
     assert [e.op for e in epi] == [R.FX_OP_ARGMAX]
-    comb = [s for s in stages if s.in_kind == R.FX_IN_COMBINE]
-    assert len(comb) == 2                     # L2.qkva and head.lm_head
-    # the combine prologue reads one x_res buffer and writes the other, alternating
-    xa, xb = host["x_res"].ptr, host["x_res_b"].ptr
-    assert {comb[0].x, comb[0].aux[2]} == {xa, xb} and comb[0].x != comb[0].aux[2]
-    assert comb[1].x == comb[0].aux[2]
-    assert host[xf].ptr == comb[1].aux[2]
-    # a plan truncated after a combine runs it standalone
-    t = G.build_plan(layers=3, head=False).truncate("L1.combine")
-    st, _, _ = B.compile_stages(t, _fake_host(t))
-    assert st[-1].op == R.FX_OP_MOE_COMBINE
-    # stage syncs: MoE layers carry 4 global and 4 XCD syncs
-    l1 = [s for s in stages if s.layer == 1]
-    assert sum(s.sync == R.FX_SYNC_GLOBAL for s in l1) + 1 == 4 + 1   # combine folded into L2.qkva
-    assert sum(s.sync == R.FX_SYNC_XCD for s in l1) == 4
+    assert n == 7 + 2 * 8 + 1            # layer 0: 7 stages, MoE layers 8 each, head 1
+    # packet sources: the embed's amax is the previous iteration's head; everything else the stage
+    # that last wrote the tensor
+    assert stages[0].src[1] == -1 and labels[-1] == "head.lm_head"
+    assert epi[0].src[0] == -1
+    for i, st in enumerate(stages):
+        if st.op == R.FX_OP_MLA_PREP:
+            assert labels[st.src[0]].endswith(".qkva") or labels[st.src[0]].endswith(".qkva+embed")
+        if st.op == R.FX_OP_MLA_ATTEND:
+            assert ops[st.src[0]] == R.FX_OP_MLA_PREP and st.src[0] == i - 1
+        if st.op == R.FX_OP_MOE_W2:
+            assert ops[st.src[0]] == R.FX_OP_MOE_W13 and ops[st.src[1]] == R.FX_OP_MOE_ROUTER
+            assert labels[st.src[2]].endswith(".o_proj") and st.out == host["x_res"].ptr and st.res == host["x_mid"].ptr
+    # layer 0's o_proj takes the embedding row as its residual; later o_projs the x_res packets
+    o0 = stages[labels.index("L0.o_proj")]
+    assert o0.flags & R.FX_F_RES_EMBED and not o0.flags & R.FX_F_RESIDUAL
+    o1 = stages[labels.index("L1.o_proj")]
+    assert o1.flags & R.FX_F_RESIDUAL and o1.res == host["x_res"].ptr and o1.out == host["x_mid"].ptr
+    assert ops[o1.src[2]] == R.FX_OP_GEMV and labels[o1.src[2]] == "L0.down"
+    # a plan truncated after a w2 keeps its combine (the same stage)
+    t = G.build_plan(layers=3, head=False).truncate("L1.w2")
+    assert t.calls[-1].label == "L1.combine"
+    st, _ = B.compile_stages(t, _fake_host(t))
+    assert st[-1].op == R.FX_OP_MOE_W2 and st[0].src[1] == -1
 
 
 def test_seeded_layout_segments_cover_each_element_once():
