@@ -221,9 +221,12 @@ __device__ __forceinline__ uint32_t pk_wait1(const void* base, uint32_t pkt, uin
   return v.x;
 }
 
-// weights: read-only for the whole dispatch, streamed once -> non-temporal 16-byte loads
-__device__ __forceinline__ u32x4 ldw16(const void* p) { return __builtin_nontemporal_load((const u32x4*)p); }
-__device__ __forceinline__ u32x4 ld16(const void* p) { return *(const u32x4*)p; }
+// weights: read-only for the whole dispatch, streamed once -> non-temporal 16-byte loads. Global
+// (address space 1) loads, not flat: a flat load also counts against the LDS counter, so every LDS
+// access would wait for the weight loads still in flight.
+typedef const __attribute__((address_space(1))) u32x4* gptr16;
+__device__ __forceinline__ u32x4 ldw16(const void* p) { return __builtin_nontemporal_load((gptr16)p); }
+__device__ __forceinline__ u32x4 ld16(const void* p) { return *(gptr16)p; }
 
 // ------------------------------------------------------------------------------------------------
 // identity
@@ -241,27 +244,58 @@ __device__ __forceinline__ int wave_id() { return threadIdx.x >> 6; }
 
 __device__ __forceinline__ float shfl_xor_f(float v, int m) { return __shfl_xor(v, m, 64); }
 
-// xor butterfly over the lowest `nl` lanes of each 64-lane group (spec order 1, 2, 4, ..)
+// Value of lane (lane ^ o) for o = 1, 2, 4, 8 (DPP inside a row of 16), 16 and 32 (the gfx950 row
+// swaps), all on the VALU: no LDS instruction, so no wait on outstanding flat/LDS counters.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+}
+template <int O>
+__device__ __forceinline__ float xor_lane(float v) {
+  if constexpr (O == 1) return dpp_mov<0xB1>(v);          // quad_perm [1,0,3,2]
+  else if constexpr (O == 2) return dpp_mov<0x4E>(v);     // quad_perm [2,3,0,1]
+  else if constexpr (O == 4) {
+    const float up = dpp_mov<0x104>(v);                   // row_shl:4  (lane + 4)
+    const float dn = dpp_mov<0x114>(v);                   // row_shr:4  (lane - 4)
+    return (threadIdx.x & 4) ? dn : up;
+  } else if constexpr (O == 8) return dpp_mov<0x128>(v);  // row_ror:8 (lane ^ 8 inside 16)
+  else if constexpr (O == 16) {
+    // odd rows of the first operand <-> even rows of the second: [0] = rows (0, 0, 2, 2), [1] = (1, 1, 3, 3)
+    const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(unsigned, v), __builtin_bit_cast(unsigned, v),
+                                                    false, false);
+    return __builtin_bit_cast(float, (threadIdx.x & 16) ? r[0] : r[1]);
+  } else {
+    // upper half of the first operand <-> lower half of the second
+    const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, v), __builtin_bit_cast(unsigned, v),
+                                                    false, false);
+    return __builtin_bit_cast(float, (threadIdx.x & 32) ? r[0] : r[1]);
+  }
+}
+
+// xor butterfly over the lowest `nl` lanes of each 64-lane group (spec order 1, 2, 4, ..): the
+// balanced pairwise tree over lanes; every lane ends with the same sum
 __device__ __forceinline__ float butterfly(float v, int nl) {
-  for (int off = 1; off < nl; off <<= 1) v = v + shfl_xor_f(v, off);
+  if (nl > 1) v = v + xor_lane<1>(v);
+  if (nl > 2) v = v + xor_lane<2>(v);
+  if (nl > 4) v = v + xor_lane<4>(v);
+  if (nl > 8) v = v + xor_lane<8>(v);
+  if (nl > 16) v = v + xor_lane<16>(v);
+  if (nl > 32) v = v + xor_lane<32>(v);
   return v;
 }
-__device__ __forceinline__ float butterfly64(float v) {
-  v = v + shfl_xor_f(v, 1);
-  v = v + shfl_xor_f(v, 2);
-  v = v + shfl_xor_f(v, 4);
-  v = v + shfl_xor_f(v, 8);
-  v = v + shfl_xor_f(v, 16);
-  v = v + shfl_xor_f(v, 32);
-  return v;
-}
+__device__ __forceinline__ float butterfly64(float v) { return butterfly(v, 64); }
 __device__ __forceinline__ int lanes_for(int nchunk) {
   int nl = 1;
   while (nl < nchunk && nl < 64) nl <<= 1;
   return nl;
 }
 __device__ __forceinline__ float wave_max(float v) {
-  for (int off = 1; off < 64; off <<= 1) v = fmaxf(v, shfl_xor_f(v, off));
+  v = fmaxf(v, xor_lane<1>(v));
+  v = fmaxf(v, xor_lane<2>(v));
+  v = fmaxf(v, xor_lane<4>(v));
+  v = fmaxf(v, xor_lane<8>(v));
+  v = fmaxf(v, xor_lane<16>(v));
+  v = fmaxf(v, xor_lane<32>(v));
   return v;
 }
 

@@ -69,12 +69,36 @@ __device__ __forceinline__ void gemv_prime(Tile<R, NJ>& t0, const uint16_t* W, i
 
 // Walk the wave's groups g = wave, wave + 4, ...; t0 holds group `wave` (gemv_prime). emit(g, rows,
 // acc) sees the R results on every lane (row < 0: no row).
+#ifndef FX_PIPE_DEPTH
+#define FX_PIPE_DEPTH 2
+#endif
 template <int R, int NJ, class RowFn, class XsFn, class EmitFn>
 __device__ __forceinline__ void gemv_pipe_x(Tile<R, NJ>& t0, const uint16_t* W, int K, XsFn xsof, int ngroups,
                                             RowFn& rowof, EmitFn emit) {
   Tile<R, NJ> t1;
   float acc[R];
   int g = wave_id();
+#if FX_PIPE_DEPTH == 3
+  // three tiles in rotation: while one is reduced, the next two are in flight
+  Tile<R, NJ> t2;
+  if (g + FX_WAVES < ngroups) tile_load(t1, W, K, g + FX_WAVES, rowof);
+  while (g < ngroups) {
+    if (g + 2 * FX_WAVES < ngroups) tile_load(t2, W, K, g + 2 * FX_WAVES, rowof);
+    tile_dot(t0, xsof(g), K, acc);
+    emit(g, t0.row, acc);
+    g += FX_WAVES;
+    if (g >= ngroups) break;
+    if (g + 2 * FX_WAVES < ngroups) tile_load(t0, W, K, g + 2 * FX_WAVES, rowof);
+    tile_dot(t1, xsof(g), K, acc);
+    emit(g, t1.row, acc);
+    g += FX_WAVES;
+    if (g >= ngroups) break;
+    if (g + 2 * FX_WAVES < ngroups) tile_load(t1, W, K, g + 2 * FX_WAVES, rowof);
+    tile_dot(t2, xsof(g), K, acc);
+    emit(g, t2.row, acc);
+    g += FX_WAVES;
+  }
+#else
   while (g < ngroups) {
     const int g1 = g + FX_WAVES;
     if (g1 < ngroups) tile_load(t1, W, K, g1, rowof);
@@ -87,6 +111,7 @@ __device__ __forceinline__ void gemv_pipe_x(Tile<R, NJ>& t0, const uint16_t* W, 
     emit(g1, t1.row, acc);
     g = g2;
   }
+#endif
 }
 // the same walk with one input row for every group
 template <int R, int NJ, class RowFn, class EmitFn>
@@ -215,9 +240,12 @@ __device__ __forceinline__ void embed_token(const void* amax, uint32_t amax_tag,
 // ------------------------------------------------------------------------------------------------
 // FX_OP_GEMV: rows in groups of 4, groups split over all workers
 
+#ifndef FX_GEMV_R
+#define FX_GEMV_R 4
+#endif
 template <int NJ>
 __device__ __forceinline__ void op_gemv_t(const fx_stage& s, FxEnv& env) {
-  constexpr int R = NJ <= 4 ? 4 : 1;
+  constexpr int R = NJ <= 4 ? FX_GEMV_R : 1;
   float* xs = (float*)(env.lds + LDS_XS);
   float* red = (float*)(env.lds + LDS_RED);
   float* rres = (float*)(env.lds + LDS_RES);
@@ -363,6 +391,18 @@ __device__ __forceinline__ void op_dense_gu(const fx_stage& s, FxEnv& env) {
   if (s.aux[6] && env.worker == 0) store_vec_sc1((void*)s.aux[6], xs, K);
   void* act = (void*)s.out;
   const uint32_t tag = tag_out(env);
-  gemv_pipe(t0, W, K, xs, ngroups, rowof, [&](int g, const int* row, const float* acc) { gate_up_emit(act, 0, row, acc, tag); });
+  // act values of the worker's groups into LDS, published after the stream
+  float* actl = (float*)(env.lds + LDS_RES);
+  gemv_pipe(t0, W, K, xs, ngroups, rowof, [&](int g, const int* row, const float* acc) {
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const float gv = bf16r(acc[2 * q]);
+      const float uv = bf16r(acc[2 * q + 1]);
+      if (lane_id() == 0) actl[2 * g + q] = row[2 * q] >= 0 ? silu_s(gv) * uv : 0.0f;
+    }
+  });
+  __syncthreads();
+  if (threadIdx.x < ngroups)
+    pk_put(act, (uint32_t)(q0 + threadIdx.x), pack2(actl[2 * threadIdx.x], actl[2 * threadIdx.x + 1]), tag);
   prof_mark(env, 2);
 }

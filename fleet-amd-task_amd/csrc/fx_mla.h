@@ -164,8 +164,7 @@ __device__ __forceinline__ void op_mla_attend(const fx_stage& s, FxEnv& env) {
   float* qp = ql + 2 * 512;                               // [2][64]
   float* sp = qp + 2 * 64;                                // [2][32][5] partial scores
   float* pb = sp + 2 * 32 * 5;                            // [2][32] bf16(p)
-  float* pp = pb + 64;                                    // [2][32] p
-  float* hs = pp + 64;                                    // [2][4] m, l, alpha, m_new
+  float* hs = pb + 64;                                    // [2][4] m, l, alpha
   uint16_t* tile = (uint16_t*)(env.lds + LDS_TILE);       // [32][ATT_ROW]
   const uint16_t* ckv = (const uint16_t*)s.aux[0];
   const uint16_t* kpe = (const uint16_t*)s.aux[1];
@@ -230,10 +229,11 @@ __device__ __forceinline__ void op_mla_attend(const fx_stage& s, FxEnv& env) {
         dst[1] = w[0].z;
       }
       __syncthreads();
-      // scores: thread (h, t, k): chain k over latent columns [128k, 128k + 128); k == 0 also the
-      // rope chain; s = ((((n0 + n1) + n2) + n3) + pe) * scale
+      // scores: thread (h, k, t): chain k over latent columns [128k, 128k + 128); k == 0 also the
+      // rope chain; s = ((((n0 + n1) + n2) + n3) + pe) * scale. Consecutive lanes take consecutive
+      // rows t (row stride 1168 B = 16 B mod 128: conflict-free b128 reads) and share q (broadcast).
       {
-        const int h = threadIdx.x >> 7, t = (threadIdx.x >> 2) & 31, k = threadIdx.x & 3;
+        const int h = threadIdx.x >> 7, k = (threadIdx.x >> 5) & 3, t = threadIdx.x & 31;
         float a = 0.0f, b = 0.0f;
         if (t < nt) {
           const uint16_t* kr = tile + t * ATT_ROW;
@@ -271,7 +271,9 @@ __device__ __forceinline__ void op_mla_attend(const fx_stage& s, FxEnv& env) {
         if (k == 0) sp[(h * 32 + t) * 5 + 4] = b;
       }
       __syncthreads();
+      if (done == 0 && t0 == lo) prof_mark(env, 4);
       // softmax of the tile on wave 0 (lane = h * 32 + t); the sum of p runs sequentially in t
+      // (lane by lane through scalar reads), then l = l * alpha + psum
       if (threadIdx.x < 64) {
         const int h = threadIdx.x >> 5, t = threadIdx.x & 31;
         float sc = -__builtin_inff();
@@ -284,37 +286,54 @@ __device__ __forceinline__ void op_mla_attend(const fx_stage& s, FxEnv& env) {
           sc = v2 * scale;
         }
         float mt = sc;
-        for (int off = 1; off < 32; off <<= 1) mt = fmaxf(mt, shfl_xor_f(mt, off));
+        mt = fmaxf(mt, xor_lane<1>(mt));
+        mt = fmaxf(mt, xor_lane<2>(mt));
+        mt = fmaxf(mt, xor_lane<4>(mt));
+        mt = fmaxf(mt, xor_lane<8>(mt));
+        mt = fmaxf(mt, xor_lane<16>(mt));
         const float m = hs[h * 4 + 0];
         const float m_new = m > mt ? m : mt;
         const float alpha = exp_s(m - m_new);
         const float p = t < nt ? exp_s(sc - m_new) : 0.0f;
-        pp[h * 32 + t] = p;
         pb[h * 32 + t] = bf16r(p);
-        if (t == 0) { hs[h * 4 + 2] = alpha; hs[h * 4 + 3] = m_new; }
+        float ps0 = 0.0f, ps1 = 0.0f;
+#pragma unroll
+        for (int u = 0; u < 32; ++u) {
+          ps0 = ps0 + __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, p), u));
+          ps1 = ps1 + __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, p), 32 + u));
+        }
+        if (t == 0) {
+          const float l = hs[h * 4 + 1];
+          hs[h * 4 + 1] = l * alpha + (h ? ps1 : ps0);
+          hs[h * 4 + 2] = alpha;
+          hs[h * 4 + 0] = m_new;
+        }
       }
       __syncthreads();
-      if (threadIdx.x < MLA_HP) {
-        const int h = threadIdx.x;
-        float psum = 0.0f;
-        for (int t = 0; t < nt; ++t) psum = psum + pp[h * 32 + t];
-        float l = hs[h * 4 + 1];
-        l = l * hs[h * 4 + 2] + psum;
-        hs[h * 4 + 1] = l;
-        hs[h * 4 + 0] = hs[h * 4 + 3];
-      }
+      if (done == 0 && t0 == lo) prof_mark(env, 5);
       // value product over the tile, sequential in t: tp[c] = sum_t bf16(p_t) v_t[c];
       // acc = acc * alpha + tp
       {
         const float alpha = hs[ph * 4 + 2];
         float tp[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        for (int t = 0; t < nt; ++t) {
-          const float pv = pb[ph * 32 + t];
-          const u32x2 kv = *(const u32x2*)(tile + t * ATT_ROW + pc);
-          tp[0] = __builtin_fmaf(pv, bf_lo(kv.x), tp[0]);
-          tp[1] = __builtin_fmaf(pv, bf_hi(kv.x), tp[1]);
-          tp[2] = __builtin_fmaf(pv, bf_lo(kv.y), tp[2]);
-          tp[3] = __builtin_fmaf(pv, bf_hi(kv.y), tp[3]);
+        // 8 rows' loads at a time, then their fmas in t order (rows past nt carry p = 0 and are
+        // skipped: their tile rows are stale)
+        for (int t8 = 0; t8 < nt; t8 += 8) {
+          u32x2 kv[8];
+          float pv[8];
+#pragma unroll
+          for (int u = 0; u < 8; ++u) {
+            kv[u] = *(const u32x2*)(tile + (t8 + u) * ATT_ROW + pc);
+            pv[u] = pb[ph * 32 + t8 + u];
+          }
+#pragma unroll
+          for (int u = 0; u < 8; ++u) {
+            if (t8 + u >= nt) break;
+            tp[0] = __builtin_fmaf(pv[u], bf_lo(kv[u].x), tp[0]);
+            tp[1] = __builtin_fmaf(pv[u], bf_hi(kv[u].x), tp[1]);
+            tp[2] = __builtin_fmaf(pv[u], bf_lo(kv[u].y), tp[2]);
+            tp[3] = __builtin_fmaf(pv[u], bf_hi(kv[u].y), tp[3]);
+          }
         }
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
@@ -323,6 +342,7 @@ __device__ __forceinline__ void op_mla_attend(const fx_stage& s, FxEnv& env) {
         }
       }
       __syncthreads();
+      if (done == 0 && t0 == lo) prof_mark(env, 6);
     }
     // o = acc / l, lse = m + log(l)
     {
@@ -341,6 +361,7 @@ __device__ __forceinline__ void op_mla_attend(const fx_stage& s, FxEnv& env) {
   // done packet: this worker's partials are complete
   wait_mem();
   __syncthreads();
+  prof_mark(env, 7);
   if (threadIdx.x == 0)
     pk_put((void*)s.aux[6], (uint32_t)(env.xcd * FX_XWORKERS + env.xrank), (uint32_t)done, tag_out(env));
   prof_mark(env, 2);
@@ -350,7 +371,7 @@ __device__ __forceinline__ void op_mla_attend(const fx_stage& s, FxEnv& env) {
 // 152-165: M = max lse, w_j = exp(lse_j - M), o = (sum_j w_j o_j, sequential fma) / (sum_j w_j,
 // sequential) -> bf16), then attn[h*d_v + v] = bf16(dot(o, W_uv[h][v])) for 8 rows v each
 // (harness/numpy_ref.py:168-174).
-#define MERGE_BATCH 16
+#define MERGE_BATCH 32
 __device__ __forceinline__ void op_mla_merge_uv(const fx_stage& s, FxEnv& env) {
   const int nh = s.n_rows, d_c = s.d_c, d_v = s.d_n, prow = s.prow;
   const int hh = env.xrank >> 4;
@@ -376,26 +397,49 @@ __device__ __forceinline__ void op_mla_merge_uv(const fx_stage& s, FxEnv& env) {
   __syncthreads();
   prof_mark(env, 1);
   const void* part = (const void*)s.x;
+  // every thread: 2 columns of o; the first 32 splits' values are requested before anything waits
+  const int pc = threadIdx.x * 2;
+  u32x2 o[MERGE_BATCH];
+#pragma unroll
+  for (int k = 0; k < MERGE_BATCH; ++k) {
+    const int j = k < live ? k : live - 1;
+    o[k] = ldc8(part, (uint32_t)((j * nh + h) * prow + pc) * 4);
+  }
+  // wave 0: lse_j, M = max lse, w_j = exp(lse_j - M) into LDS, den = sum_j w_j in j order
   if (wave_id() == 0) {
-    float mx = -__builtin_inff();
-    for (int j = lane_id(); j < live; j += 64) mx = fmaxf(mx, ldcf(part, (uint32_t)((j * nh + h) * prow + d_c)));
+    // lse of splits lane, lane + 64 (one load each), then the rest (more than 128 splits) from LDS
+    float l0 = -__builtin_inff(), l1 = -__builtin_inff();
+    if (lane_id() < live) l0 = ldcf(part, (uint32_t)((lane_id() * nh + h) * prow + d_c));
+    if (lane_id() + 64 < live) l1 = ldcf(part, (uint32_t)(((lane_id() + 64) * nh + h) * prow + d_c));
+    float mx = fmaxf(l0, l1);
+    for (int j = lane_id() + 128; j < live; j += 64) {
+      const float v = ldcf(part, (uint32_t)((j * nh + h) * prow + d_c));
+      wj[j] = v;
+      mx = fmaxf(mx, v);
+    }
     mx = wave_max(mx);
-    for (int j = lane_id(); j < live; j += 64) wj[j] = exp_s(ldcf(part, (uint32_t)((j * nh + h) * prow + d_c)) - mx);
+    float den = 0.0f;
+    for (int j0 = 0; j0 < live; j0 += 64) {
+      const int j = j0 + lane_id();
+      const float lse = j0 == 0 ? l0 : (j0 == 64 ? l1 : (j < live ? wj[j] : -__builtin_inff()));
+      const float w = j < live ? exp_s(lse - mx) : 0.0f;
+      if (j < live) wj[j] = w;
+      const int n = live - j0 < 64 ? live - j0 : 64;
+      for (int u = 0; u < n; ++u) den = den + __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), u));
+    }
+    if (lane_id() == 0) red[0] = den;
   }
   __syncthreads();
-  if (threadIdx.x == 0) {
-    float den = 0.0f;
-    for (int j = 0; j < live; ++j) den = den + wj[j];
-    red[0] = den;
-  }
-  const int pc = threadIdx.x * 2;
+  prof_mark(env, 4);
+  // num = sum_j w_j o_j[c] in j order (fma)
   float num[2] = {0.0f, 0.0f};
   for (int j0 = 0; j0 < live; j0 += MERGE_BATCH) {
-    u32x2 o[MERGE_BATCH];
+    if (j0 > 0) {
 #pragma unroll
-    for (int k = 0; k < MERGE_BATCH; ++k) {
-      const int j = j0 + k < live ? j0 + k : live - 1;
-      o[k] = ldc8(part, (uint32_t)((j * nh + h) * prow + pc) * 4);
+      for (int k = 0; k < MERGE_BATCH; ++k) {
+        const int j = j0 + k < live ? j0 + k : live - 1;
+        o[k] = ldc8(part, (uint32_t)((j * nh + h) * prow + pc) * 4);
+      }
     }
 #pragma unroll
     for (int k = 0; k < MERGE_BATCH; ++k) {
@@ -411,6 +455,7 @@ __device__ __forceinline__ void op_mla_merge_uv(const fx_stage& s, FxEnv& env) {
   xs[pc + 1] = bf16r(num[1] / den);
   if ((env.xrank & 15) == 0 && s.aux[4]) stc4((void*)s.aux[4], (uint32_t)(h * d_c + pc) * 2, pack2(xs[pc], xs[pc + 1]));
   __syncthreads();
+  prof_mark(env, 5);
   float* o8 = red + 16;
   gemv_pipe(t0, W, d_c, xs, ngroups, rowof, [&](int g, const int* row, const float* acc) {
 #pragma unroll

@@ -1,9 +1,9 @@
 // MoE operators: router, expert gate|up + SiLU, expert down fused with the combine; the argmax
 // reduce. harness/numpy_ref.py:205-292, 316-321; the reference's moe_router_mi300.cuh:115-354,
 // gang_moe_w13_gemv_mi300.cuh:101-219, gang_moe_w2_silu_mi300.cuh and moe_mul_sum_add.
-// Slot s of the 8 (top-6 routed, then the two shared experts E, E+1 at weight 1.0): its gate|up
-// runs on XCD s; its down projection is spread over every worker (8 output rows each, all slots),
-// so the combine of a row happens where its eight slot values are.
+// Slot s of the 8 (top-6 routed, then the two shared experts E, E+1 at weight 1.0). Gate|up and down
+// are both spread over every worker for every slot (pair groups / 8 output rows each), shared slots
+// first; the combine of a row happens where its eight slot values are.
 #pragma once
 #include "fx_gemv.h"
 
@@ -77,92 +77,129 @@ __device__ __forceinline__ void op_moe_router(const fx_stage& s, FxEnv& env) {
   prof_mark(env, 2);
 }
 
-// FX_OP_MOE_W13: slot = XCD; the slot's expert from the router logits (routed slots) or fixed
-// (shared slots), then act8[slot][i] = bf16(silu(bf16(W13[e][i] h)) * bf16(W13[e][I + i] h)) over
-// the XCD's 32 workers. A shared slot issues its weight loads before anything arrives.
+// FX_OP_MOE_W13 over every worker: worker w owns pair groups [q0, q1) (2 pairs each) of every slot's
+// expert; shared slots first, so their weights stream while the router logits are still on their
+// way. With FX_F_ROUTER the stage also computes the router (row e on worker e, W_gate in `res`) and
+// reads the logits back from its own packets. act8[slot][i] = bf16(silu(bf16(W13[e][i] h)) *
+// bf16(W13[e][I + i] h)).
 __device__ __forceinline__ void op_moe_w13(const fx_stage& s, FxEnv& env) {
   float* xs = (float*)(env.lds + LDS_XS);
   float* red = (float*)(env.lds + LDS_RED);
-  int* misc = (int*)(env.lds + LDS_MISC);
   int* ids = (int*)(env.lds + LDS_MISC + 128);
   float* wts = (float*)(env.lds + LDS_MISC + 256);
   const int K = s.k, I = s.n_rows, E = s.aux_i0;
-  const int slot = env.xcd;
-  const int topk = s.topk;
-  const bool routed = slot < topk;
+  const int topk = s.topk, nsh = s.n_forced;
+  const bool router = (s.flags & FX_F_ROUTER) != 0;
   const bool writer = env.worker == 0;
   float* lg = red + 256;
-  PairRows rowof;
   int q0, q1;
-  range_split(I >> 1, env.xworkers, env.xrank, q0, q1);
-  rowof.p0 = 2 * q0;
-  rowof.p1 = 2 * q1;
-  rowof.I = I;
-  const int ngroups = q1 - q0;
+  range_split(I >> 1, env.nworkers, env.worker, q0, q1);
+  const int nq = q1 - q0;
+  const int nA = nsh * nq, nB = topk * nq;
+  const uint16_t* W = (const uint16_t*)s.w;
+  const size_t ex = (size_t)2 * I;   // rows per expert
+  auto rowA = [&](int g, int i) {
+    const int e = E + g / nq;
+    const int p = 2 * (q0 + g % nq) + (i >> 1);
+    return (int)(e * ex + ((i & 1) ? I + p : p));
+  };
+  auto rowB = [&](int g, int i) {
+    const int e = ids[g / nq];
+    const int p = 2 * (q0 + g % nq) + (i >> 1);
+    return (int)(e * ex + ((i & 1) ? I + p : p));
+  };
   Tile<4, 4> t0;
-  const uint16_t* W = nullptr;
-  if (!routed) {
-    W = (const uint16_t*)s.w + (size_t)(E + slot - topk) * 2 * I * K;
-    gemv_prime(t0, W, K, ngroups, rowof);
-  }
-  if ((routed || writer) && wave_id() == 0) poll_logits_wave(lg, (const void*)s.aux[0], E, tag_in(s, env, 0), env.err);
+  gemv_prime(t0, W, K, nA, rowA);
+  const bool rrow = router && env.worker < E;
+  const uint16_t* Wg = (const uint16_t*)s.res;
+  auto rowR = [&](int g, int i) { return env.worker; };
+  Tile<1, 4> tr;
+  if (rrow && wave_id() == 0) tile_load(tr, Wg, K, 0, rowR);
   poll_row(xs, (const void*)s.x, K, tag_in(s, env, 1), env.err);
   prof_mark(env, 1);
-  __syncthreads();
-  if (wave_id() == 0) {
-    int e = E + (slot - topk);
-    if (routed || writer) {
-      float* probs = red + 512;
-      route_slots_wave(lg, s, ids, wts, probs);
-      if (routed) e = ids[slot];
-      if (writer) {
-        // router outputs in numpy_ref.moe_router's layout: topk_w, routing, mask, logits, route_log
-        const int n_slots = s.n_slots, n_total = E + s.n_forced;
-        const int lane = lane_id();
-        const int row = env.step - (env.n_prompt - 1);
-        for (int k = lane; k < n_slots; k += 64) {
-          stcf((void*)s.aux[1], k, wts[k]);
-          // route_log [prow][aux_i1][n_slots] at row step - (n_prompt - 1): the decode iterations,
-          // as the reference logs them (route_log [32, 26, 8] at [step - 1023])
-          if (s.aux[5] && s.layer >= 1 && row >= 0 && row < s.prow)
-            stc4((void*)s.aux[5], (uint32_t)(((row * s.aux_i1) + (s.layer - 1)) * n_slots + k) * 4, (uint32_t)ids[k]);
-        }
-        for (int x = lane; x < n_total; x += 64) {
-          int r = 0;
-          for (int k = 0; k < n_slots; ++k)
-            if (ids[k] == x) r = k + 1;
-          stc4((void*)s.aux[2], x * 4, (uint32_t)r);
-        }
-        for (int x = lane; x <= n_total; x += 64) {
-          int v = -1;
-          if (x < n_slots) v = ids[x];
-          if (x == n_total) v = n_slots;
-          stc4((void*)s.aux[3], x * 4, (uint32_t)v);
-        }
-        for (int x = lane; x < E; x += 64) stcf((void*)s.aux[4], x, lg[x]);
-      }
-    }
-    if (lane_id() == 0) misc[0] = e;
-    if (env.xrank == 0 && lane_id() == 0 && s.aux[7]) stc4((void*)s.aux[7], slot * 4, (uint32_t)e);
-  }
-  __syncthreads();
-  if (routed) {
-    W = (const uint16_t*)s.w + (size_t)misc[0] * 2 * I * K;
-    gemv_prime(t0, W, K, ngroups, rowof);
-  }
   rmsnorm_inplace(xs, (const uint16_t*)s.w_norm, K, s.eps, red);
-  if (s.aux[6] && writer) store_vec_sc1((void*)s.aux[6], xs, K);
-  void* act = (void*)s.out;
-  const uint32_t base = (uint32_t)slot * (I >> 1);
   const uint32_t tag = tag_out(env);
-  gemv_pipe(t0, W, K, xs, ngroups, rowof, [&](int g, const int* row, const float* acc) { gate_up_emit(act, base, row, acc, tag); });
+  if (rrow && wave_id() == 0) {
+    float acc[1];
+    tile_dot(tr, xs, K, acc);
+    if (lane_id() == 0) pk_put((void*)s.aux[0], (uint32_t)env.worker, __float_as_uint(acc[0]), tag);
+  }
+  if (s.aux[6] && writer) store_vec_sc1((void*)s.aux[6], xs, K);
+  prof_mark(env, 4);
+  void* act = (void*)s.out;
+  const int half = I >> 1;
+  // act values of the worker's groups: LDS [slot][nq][2], published after the stream
+  float* actl = (float*)(env.lds + LDS_RES);
+  auto emit = [&](int slot_base, int g, const float* acc) {
+    float a[2];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const float gv = bf16r(acc[2 * q]);
+      const float uv = bf16r(acc[2 * q + 1]);
+      a[q] = silu_s(gv) * uv;
+    }
+    if (lane_id() == 0) {
+      const int i = (slot_base + g / nq) * nq + g % nq;
+      actl[2 * i] = a[0];
+      actl[2 * i + 1] = a[1];
+    }
+  };
+  gemv_pipe(t0, W, K, xs, nA, rowA, [&](int g, const int* row, const float* acc) { emit(topk, g, acc); });
+  __syncthreads();
+  if (threadIdx.x < nA) {
+    const int i = topk * nq + threadIdx.x;
+    pk_put(act, (uint32_t)((topk + threadIdx.x / nq) * half + q0 + threadIdx.x % nq), pack2(actl[2 * i], actl[2 * i + 1]),
+           tag);
+  }
+  prof_mark(env, 5);
+  // routed slots: the top-k of the logits
+  if (wave_id() == 0) {
+    poll_logits_wave(lg, (const void*)s.aux[0], E, router ? tag : tag_in(s, env, 0), env.err);
+    float* probs = red + 512;
+    route_slots_wave(lg, s, ids, wts, probs);
+    if (writer) {
+      // router outputs in numpy_ref.moe_router's layout: topk_w, routing, mask, logits, route_log, sel
+      const int n_slots = s.n_slots, n_total = E + s.n_forced;
+      const int lane = lane_id();
+      const int row = env.step - (env.n_prompt - 1);
+      for (int k = lane; k < n_slots; k += 64) {
+        stcf((void*)s.aux[1], k, wts[k]);
+        if (s.aux[7]) stc4((void*)s.aux[7], k * 4, (uint32_t)ids[k]);
+        // route_log [prow][aux_i1][n_slots] at row step - (n_prompt - 1): the decode iterations,
+        // as the reference logs them (route_log [32, 26, 8] at [step - 1023])
+        if (s.aux[5] && s.layer >= 1 && row >= 0 && row < s.prow)
+          stc4((void*)s.aux[5], (uint32_t)(((row * s.aux_i1) + (s.layer - 1)) * n_slots + k) * 4, (uint32_t)ids[k]);
+      }
+      for (int x = lane; x < n_total; x += 64) {
+        int r = 0;
+        for (int k = 0; k < n_slots; ++k)
+          if (ids[k] == x) r = k + 1;
+        stc4((void*)s.aux[2], x * 4, (uint32_t)r);
+      }
+      for (int x = lane; x <= n_total; x += 64) {
+        int v = -1;
+        if (x < n_slots) v = ids[x];
+        if (x == n_total) v = n_slots;
+        stc4((void*)s.aux[3], x * 4, (uint32_t)v);
+      }
+      for (int x = lane; x < E; x += 64) stcf((void*)s.aux[4], x, lg[x]);
+    }
+  }
+  __syncthreads();
+  prof_mark(env, 6);
+  gemv_prime(t0, W, K, nB, rowB);
+  gemv_pipe(t0, W, K, xs, nB, rowB, [&](int g, const int* row, const float* acc) { emit(0, g, acc); });
+  __syncthreads();
+  if (threadIdx.x < nB)
+    pk_put(act, (uint32_t)((threadIdx.x / nq) * half + q0 + threadIdx.x % nq),
+           pack2(actl[2 * threadIdx.x], actl[2 * threadIdx.x + 1]), tag);
   prof_mark(env, 2);
 }
 
 // FX_OP_MOE_W2 with the combine: worker w owns output rows [r0, r0 + 8) of every slot; group g is
-// 4 rows of one slot (shared slots first, so their loads go out before the logits arrive);
-// x_new[n] = bf16(x[n] + sum_s out8[s][n] * w_s), multiply then add, in slot order
-// (harness/numpy_ref.py:316-321).
+// 4 rows of one slot. The shared slots' activations (finished first by the gate|up stage) are
+// awaited and consumed first, then the routed ones; x_new[n] = bf16(x[n] + sum_s out8[s][n] * w_s),
+// multiply then add, in slot order (harness/numpy_ref.py:316-321).
 #define W2_ROWS 8
 __device__ __forceinline__ void op_moe_w2(const fx_stage& s, FxEnv& env) {
   float* xs = (float*)(env.lds + LDS_XS);        // act8 [8][I]
@@ -172,25 +209,19 @@ __device__ __forceinline__ void op_moe_w2(const fx_stage& s, FxEnv& env) {
   float* rres = (float*)(env.lds + LDS_RES);     // x rows [8], then out8 [8 slots][8 rows] at +16
   const int I = s.k, H = s.n_rows;
   const int nslots = FX_SLOTS;
-  const int nsh = s.n_forced;
+  const int nsh = s.n_forced, topk = s.topk;
   const int E = s.aux_i0;
   int c0, c1;
   range_split(H / W2_ROWS, env.nworkers, env.worker, c0, c1);
   const int r0 = c0 * W2_ROWS;
   const int nrow = (c1 - c0) * W2_ROWS;          // 8 (H = 2048, 256 workers)
   const int quads = nrow >> 2;
-  const int ngroups = nslots * quads;
-  // group g -> slot (shared first), quad
-  auto slot_of = [&](int g) { const int k = g / quads; return k < nsh ? s.topk + k : k - nsh; };
-  auto rowof = [&](int g, int i) {
-    const int sl = slot_of(g);
-    const int e = sl < s.topk ? ids[sl] : E + (sl - s.topk);
-    return e * H + r0 + (g % quads) * 4 + i;
-  };
+  const int nA = nsh * quads, nB = topk * quads;
   const uint16_t* W = (const uint16_t*)s.w;
+  auto rowA = [&](int g, int i) { return (E + g / quads) * H + r0 + (g % quads) * 4 + i; };
+  auto rowB = [&](int g, int i) { return ids[g / quads] * H + r0 + (g % quads) * 4 + i; };
   Tile<4, 3> t0;
-  // shared-slot groups first: wave v's first group is v, a shared slot when v < nsh * quads
-  if (wave_id() < nsh * quads) tile_load(t0, W, I, wave_id(), rowof);
+  gemv_prime(t0, W, I, nA, rowA);
   if (wave_id() == 0) {
     float* lg = red + 256;
     poll_logits_wave(lg, (const void*)s.aux[0], E, tag_in(s, env, 1), env.err);
@@ -205,20 +236,29 @@ __device__ __forceinline__ void op_moe_w2(const fx_stage& s, FxEnv& env) {
     rres[i + 2] = bf_lo(v[0].z);
     rres[i + 3] = bf_hi(v[0].z);
   }
-  __syncthreads();
-  if (wave_id() >= nsh * quads && wave_id() < ngroups) tile_load(t0, W, I, wave_id(), rowof);
-  poll_row(xs, (const void*)s.x, nslots * I, tag_in(s, env, 0), env.err);
+  // shared slots' activations (slots topk .. topk + nsh - 1 of act8)
+  const uint32_t tact = tag_in(s, env, 0);
+  poll_row(xs + topk * I, (const uint8_t*)s.x + (size_t)topk * I * 4, nsh * I, tact, env.err);
   prof_mark(env, 1);
   __syncthreads();
   float* o8 = rres + 16;
-  gemv_pipe_x(t0, W, I, [&](int g) { return (const float*)(xs + slot_of(g) * I); }, ngroups, rowof,
-              [&](int g, const int* row, const float* acc) {
-                if (lane_id() == 0) {
-                  const int sl = slot_of(g);
+  auto emit = [&](int slot_base, int g, const float* acc) {
+    if (lane_id() == 0) {
+      const int sl = slot_base + g / quads;
 #pragma unroll
-                  for (int i = 0; i < 4; ++i) o8[sl * W2_ROWS + (g % quads) * 4 + i] = bf16r(acc[i]);
-                }
-              });
+      for (int i = 0; i < 4; ++i) o8[sl * W2_ROWS + (g % quads) * 4 + i] = bf16r(acc[i]);
+    }
+  };
+  gemv_pipe_x(t0, W, I, [&](int g) { return (const float*)(xs + (topk + g / quads) * I); }, nA, rowA,
+              [&](int g, const int* row, const float* acc) { emit(topk, g, acc); });
+  prof_mark(env, 4);
+  // routed slots
+  gemv_prime(t0, W, I, nB, rowB);
+  poll_row(xs, (const void*)s.x, topk * I, tact, env.err);
+  __syncthreads();
+  prof_mark(env, 5);
+  gemv_pipe_x(t0, W, I, [&](int g) { return (const float*)(xs + (g / quads) * I); }, nB, rowB,
+              [&](int g, const int* row, const float* acc) { emit(0, g, acc); });
   __syncthreads();
   if (threadIdx.x < nrow) {
     const int r = threadIdx.x;

@@ -15,8 +15,11 @@ typedef uint32_t u32x4p __attribute__((ext_vector_type(4)));
 
 // ---- stream: block b reads [b * bytes, (b + 1) * bytes) of src with the GEMV pattern: each wave
 // issues `depth` 1 KiB loads (64 lanes x 16 B) before consuming them; stamps per block.
+// pattern 0: load d of a wave reads the d-th KiB of its D KiB block; pattern 1: the GEMV tile order,
+// D / 4 KiB-chunks of 4 rows of 4 KiB, chunk-major (load d: row d % 4, KiB d / 4); pattern 2: as 1
+// with rows 2, 3 taken from the second half of the block (two streams, the gate | up pair layout).
 template <int D>
-__device__ void stream_body(const uint8_t* src, uint64_t bytes, uint64_t* ticks, uint32_t* sink) {
+__device__ void stream_body(const uint8_t* src, uint64_t bytes, uint64_t* ticks, uint32_t* sink, int pattern) {
   const uint8_t* base = src + (uint64_t)blockIdx.x * bytes;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
   const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
@@ -26,7 +29,14 @@ __device__ void stream_body(const uint8_t* src, uint64_t bytes, uint64_t* ticks,
     u32x4p v[D];
 #pragma unroll
     for (int d = 0; d < D; ++d) {
-      uint64_t o = off + (uint64_t)d * 1024 + lane * 16;
+      uint64_t o;
+      if (pattern == 0) o = off + (uint64_t)d * 1024;
+      else if (pattern == 1) o = off + (uint64_t)(d % 4) * (D / 4) * 1024 + (uint64_t)(d / 4) * 1024;
+      else {
+        const int r = d % 4;
+        o = (off >> 1) + (uint64_t)(r >> 1) * (bytes >> 1) + (uint64_t)(r & 1) * (D / 4) * 1024 + (uint64_t)(d / 4) * 1024;
+      }
+      o += lane * 16;
       if (o + 16 > bytes) o = lane * 16;
       v[d] = __builtin_nontemporal_load((const u32x4p*)(base + o));
     }
@@ -38,12 +48,58 @@ __device__ void stream_body(const uint8_t* src, uint64_t bytes, uint64_t* ticks,
   if (acc == 0x12345678u) sink[0] = acc;
 }
 
-__global__ void fxp_stream_kernel(const uint8_t* src, uint64_t bytes, int depth, uint64_t* ticks, uint32_t* sink) {
+// double-buffered walk (the GEMV pipeline): tile = D loads of 1 KiB; the next tile is issued before
+// the current one is consumed, so between D and 2D loads are in flight per wave
+template <int D>
+__device__ void stream_db(const uint8_t* src, uint64_t bytes, uint64_t* ticks, uint32_t* sink) {
+  const uint8_t* base = src + (uint64_t)blockIdx.x * bytes;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+  uint32_t acc = 0;
+  const uint64_t step = (uint64_t)nw * D * 1024;
+  auto load = [&](u32x4p* v, uint64_t off) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      uint64_t o = off + (uint64_t)d * 1024 + lane * 16;
+      if (o + 16 > bytes) o = lane * 16;
+      v[d] = __builtin_nontemporal_load((const u32x4p*)(base + o));
+    }
+  };
+  auto use = [&](const u32x4p* v) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) acc += v[d].x ^ v[d].y ^ v[d].z ^ v[d].w;
+  };
+  u32x4p a[D], b[D];
+  uint64_t off = (uint64_t)wave * D * 1024;
+  if (off < bytes) load(a, off);
+  while (off < bytes) {
+    const uint64_t o1 = off + step;
+    if (o1 < bytes) load(b, o1);
+    use(a);
+    if (o1 >= bytes) break;
+    const uint64_t o2 = o1 + step;
+    if (o2 < bytes) load(a, o2);
+    use(b);
+    off = o2;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) ticks[blockIdx.x] = __builtin_amdgcn_s_memrealtime() - t0;
+  if (acc == 0x12345678u) sink[0] = acc;
+}
+
+__global__ void fxp_stream_kernel(const uint8_t* src, uint64_t bytes, int depth, uint64_t* ticks, uint32_t* sink,
+                                  int pattern) {
+  if (pattern == 3) {
+    if (depth == 4) stream_db<4>(src, bytes, ticks, sink);
+    else if (depth == 8) stream_db<8>(src, bytes, ticks, sink);
+    else stream_db<16>(src, bytes, ticks, sink);
+    return;
+  }
   switch (depth) {
-    case 4: stream_body<4>(src, bytes, ticks, sink); break;
-    case 8: stream_body<8>(src, bytes, ticks, sink); break;
-    case 16: stream_body<16>(src, bytes, ticks, sink); break;
-    default: stream_body<32>(src, bytes, ticks, sink); break;
+    case 4: stream_body<4>(src, bytes, ticks, sink, pattern); break;
+    case 8: stream_body<8>(src, bytes, ticks, sink, pattern); break;
+    case 16: stream_body<16>(src, bytes, ticks, sink, pattern); break;
+    default: stream_body<32>(src, bytes, ticks, sink, pattern); break;
   }
 }
 
@@ -139,11 +195,24 @@ __global__ void fxp_pingpong_kernel(uint32_t* flag, int a, int b, uint32_t round
   if (acc == 0x12345678u) out[2] = acc;
 }
 
+// ---- lane exchange check: out[lane * 6 + k] = the value xor_lane<2^k> returns on `lane` when every
+// lane holds its own index (must be lane ^ 2^k)
+__global__ void fxp_lanes_kernel(float* out) {
+  const float v = (float)(threadIdx.x & 63);
+  const int l = threadIdx.x & 63;
+  out[l * 6 + 0] = xor_lane<1>(v);
+  out[l * 6 + 1] = xor_lane<2>(v);
+  out[l * 6 + 2] = xor_lane<4>(v);
+  out[l * 6 + 3] = xor_lane<8>(v);
+  out[l * 6 + 4] = xor_lane<16>(v);
+  out[l * 6 + 5] = xor_lane<32>(v);
+}
+
 extern "C" {
 
 // all functions: 0 on success, else the hipError_t value
-int fxp_stream(const void* src, uint64_t bytes_per_block, int blocks, int threads, int depth, uint64_t* ticks_host,
-               float* ms) {
+int fxp_stream(const void* src, uint64_t bytes_per_block, int blocks, int threads, int depth, int pattern,
+               uint64_t* ticks_host, float* ms) {
   uint64_t* d_ticks = nullptr;
   uint32_t* sink = nullptr;
   hipEvent_t e0, e1;
@@ -154,7 +223,7 @@ int fxp_stream(const void* src, uint64_t bytes_per_block, int blocks, int thread
   (void)hipEventCreate(&e1);
   (void)hipEventRecord(e0, 0);
   hipLaunchKernelGGL(fxp_stream_kernel, dim3(blocks), dim3(threads), 0, 0, (const uint8_t*)src, bytes_per_block, depth,
-                     d_ticks, sink);
+                     d_ticks, sink, pattern);
   (void)hipEventRecord(e1, 0);
   if ((e = hipEventSynchronize(e1)) != hipSuccess) return e;
   (void)hipEventElapsedTime(ms, e0, e1);
@@ -200,6 +269,17 @@ int fxp_pingpong(int a, int b, uint32_t rounds, const void* load, uint64_t load_
   e = hipMemcpy(out_host, out, 24, hipMemcpyDeviceToHost);
   (void)hipFree(flag);
   (void)hipFree(out);
+  return e;
+}
+
+int fxp_lanes(float* out_host) {
+  float* d = nullptr;
+  hipError_t e;
+  if ((e = hipMalloc(&d, 64 * 6 * 4)) != hipSuccess) return e;
+  hipLaunchKernelGGL(fxp_lanes_kernel, dim3(1), dim3(64), 0, 0, d);
+  if ((e = hipDeviceSynchronize()) != hipSuccess) return e;
+  e = hipMemcpy(out_host, d, 64 * 6 * 4, hipMemcpyDeviceToHost);
+  (void)hipFree(d);
   return e;
 }
 

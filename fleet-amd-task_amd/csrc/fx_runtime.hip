@@ -411,8 +411,10 @@ static int check_stage(fx_ctx* c, const fx_stage& s, int idx, int n_total) {
       if (!s.w || !s.x || !s.out || !s.w_norm || !s.aux[0] || !s.aux[1] || !s.aux[2] || !s.aux[3] || !s.aux[4])
         return bad("w13 pointers");
       if (s.n_slots != FX_XCDS || s.topk + s.n_forced != s.n_slots || s.aux_i0 > 64 || s.aux_i0 % 2 || s.k != 2048 ||
-          s.n_rows % 4 || (s.n_rows / 2) % FX_XWORKERS)
+          s.n_rows % 4)
         return bad("w13 shape");
+      if ((s.flags & FX_F_ROUTER) && !s.res) return bad("w13 router weights");
+      if (((s.n_rows / 2 + FX_WORKERS - 1) / FX_WORKERS) * s.n_slots > 64) return bad("w13 groups per worker");
       break;
     case FX_OP_MOE_W2:
       if (!s.w || !s.x || !s.out || !s.res || !s.aux[0] || (s.k / 8 + 63) / 64 > 3 || s.k % 8) return bad("w2");
@@ -420,7 +422,8 @@ static int check_stage(fx_ctx* c, const fx_stage& s, int idx, int n_total) {
       if (s.n_rows != 8 * FX_WORKERS || s.n_slots * s.k > 11264) return bad("w2 rows / input row");
       break;
     case FX_OP_DENSE_GU:
-      if (!s.w || !s.x || !s.out || !s.w_norm || s.k != 2048 || s.n_rows % 2) return bad("dense gate/up");
+      if (!s.w || !s.x || !s.out || !s.w_norm || s.k != 2048 || s.n_rows % 4) return bad("dense gate/up");
+      if (2 * ((s.n_rows / 2 + FX_WORKERS - 1) / FX_WORKERS) > FX_MAX_OUT_ROWS) return bad("dense gate/up rows per worker");
       break;
     case FX_OP_ARGMAX:
       if (!s.aux[3] || !s.aux[4]) return bad("argmax");
@@ -582,6 +585,36 @@ int fx_run_stage(fx_ctx* c, const fx_stage* st, int32_t step, uint32_t tbase, in
   uint32_t err = 0;
   HIPCHK(c, hipMemcpy(&err, c->err_flag, 4, hipMemcpyDeviceToHost));
   if (err) return fail(c, FX_E_STATE, "a packet wait timed out in the stage launch; create a new context");
+  return FX_OK;
+}
+
+int fx_time_stages(fx_ctx* c, const fx_stage* st, int32_t n, int32_t reps, int32_t step, uint32_t tbase, int32_t sidx,
+                   void* stream, float* us) {
+  if (!c || !st || n <= 0 || reps <= 0 || !us) return fail(c, FX_E_ARG, "time_stages arguments");
+  for (int i = 0; i < n; ++i) {
+    int r = check_stage(c, st[i], i, 1 << 20);
+    if (r) return r;
+  }
+  hipStream_t s = (hipStream_t)stream;
+  int n_prompt = 1 << 30;
+  HIPCHK(c, hipEventRecord(c->ev0, s));
+  for (int rep = 0; rep < reps; ++rep)
+    for (int i = 0; i < n; ++i) {
+      const bool uses_tokens = st[i].op == FX_OP_ARGMAX ||
+                               (st[i].op == FX_OP_GEMV && (st[i].in_kind == FX_IN_EMBED || (st[i].flags & FX_F_RES_EMBED)));
+      int64_t* tokens = uses_tokens ? (int64_t*)st[i].aux[4] : nullptr;
+      void* args[] = {(void*)&st[i], &step, &n_prompt, &tbase, &sidx, &tokens, &c->err_flag};
+      HIPCHK(c, hipLaunchCooperativeKernel((const void*)fx_stage_kernel, dim3(FX_BLOCKS), dim3(FX_THREADS), args,
+                                           FX_LDS_BYTES, s));
+    }
+  HIPCHK(c, hipEventRecord(c->ev1, s));
+  HIPCHK(c, hipEventSynchronize(c->ev1));
+  float ms = 0.0f;
+  HIPCHK(c, hipEventElapsedTime(&ms, c->ev0, c->ev1));
+  *us = 1000.0f * ms / (float)(reps * n);
+  uint32_t err = 0;
+  HIPCHK(c, hipMemcpy(&err, c->err_flag, 4, hipMemcpyDeviceToHost));
+  if (err) return fail(c, FX_E_STATE, "a packet wait timed out in a timed stage launch; create a new context");
   return FX_OK;
 }
 

@@ -7,6 +7,8 @@ is validated and uploaded by fx_load_plan -- no code generation. Three calls are
 neighbour (no stage of their own):
   prologue.embed     -> L0.qkva reads W_embed[tokens[step]] (or, once past the prompt, the previous
                         head's argmax); L0.o_proj takes the same row as its residual;
+  L{l}.router        -> L{l}.w13 (FX_F_ROUTER): worker e computes router row e inside the gate|up
+                        stage, whose shared-expert weights stream meanwhile;
   L{l}.combine       -> L{l}.w2: each worker computes its 8 output rows for every slot and combines
                         them with the residual;
   head.argmax_reduce -> the next iteration's embed; the last iteration's runs as the epilogue.
@@ -47,6 +49,7 @@ def compile_stages(plan, host):
     stages, epi, labels = [], [], []
     reads = []          # per stage: [(src slot, tensor name)]
     pend_embed = None
+    pend_router = None
     B = lambda n: host[n].ptr if n else 0
 
     def add(st, label, ins):
@@ -63,6 +66,11 @@ def compile_stages(plan, host):
         if m == "moe_mul_sum_add_layer":
             assert stages and stages[-1].op == R.FX_OP_MOE_W2, "combine must follow its w2"
             continue
+        if m == "moe_router_layer":
+            pend_router = c
+            continue
+        if pend_router is not None and m != "gang_moe_w13_gemv_layer":
+            raise ValueError("the router must be followed by its w13")
         if m == "argmax_reduce_layer":
             epi.append((_stage(op=R.FX_OP_ARGMAX, aux={3: B(a["input"]), 4: B("tokens")}), [(0, a["input"])]))
             continue
@@ -131,10 +139,6 @@ def compile_stages(plan, host):
             st = _stage(op=R.FX_OP_DENSE_GU, n_rows=d.I_DENSE, k=d.H, x=B(a["input"]), w_norm=B(a["w_norm"]),
                         w=B(a["weight"]), out=B(a["output"]), aux={6: B(a.get("h"))}, **common)
             ins = [(0, a["input"])]
-        elif m == "moe_router_layer":
-            st = _stage(op=R.FX_OP_MOE_ROUTER, n_rows=d.E, k=d.H, topk=d.TOPK, x=B(a["input"]), w_norm=B(a["w_norm"]),
-                        w=B(a["w_gate"]), out=B(a["logits_x"]), **common)
-            ins = [(0, a["input"])]
         elif m == "gang_moe_w13_gemv_layer":
             rl = host[a["route_log"]]
             st = _stage(op=R.FX_OP_MOE_W13, n_rows=d.I_MOE, k=d.H, n_slots=d.N_SLOTS, topk=d.TOPK,
@@ -142,7 +146,18 @@ def compile_stages(plan, host):
                         prow=rl.shape[0], x=B(a["input"]), w_norm=B(a["w_norm"]), w=B(a["weight"]), out=B(a["output"]),
                         aux={0: B(a["logits_x"]), 1: B(a["topk_w"]), 2: B(a["routing"]), 3: B(a["mask"]),
                              4: B(a["logits"]), 5: rl.ptr, 6: B(a["h"]), 7: B(a["sel"])}, **common)
-            ins = [(0, a["logits_x"]), (1, a["input"])]
+            ins = [(1, a["input"])]
+            lab = c.label
+            if pend_router is not None:
+                assert pend_router.args["w_norm"] == a["w_norm"] and pend_router.args["logits_x"] == a["logits_x"]
+                st.flags |= R.FX_F_ROUTER
+                st.res = B(pend_router.args["w_gate"])
+                lab = c.label + "+router"
+                pend_router = None
+            else:
+                ins.append((0, a["logits_x"]))
+            add(st, lab, ins)
+            continue
         elif m == "gang_moe_w2_linear_layer":
             comb = next(cc for cc in plan.calls if cc.label == c.label.replace(".w2", ".combine"))
             st = _stage(op=R.FX_OP_MOE_W2, n_rows=d.H, k=d.I_MOE, n_slots=d.N_SLOTS, topk=d.TOPK, n_forced=d.N_SHARED,
@@ -154,6 +169,11 @@ def compile_stages(plan, host):
             raise ValueError(f"unknown plan method {m}")
         add(st, c.label, ins)
     assert pend_embed is None, "a plan cannot end on prologue.embed"
+    if pend_router is not None:     # a plan truncated after L{l}.router: the router alone
+        a = pend_router.args
+        add(_stage(op=R.FX_OP_MOE_ROUTER, n_rows=d.E, k=d.H, topk=d.TOPK, x=B(a["input"]), w_norm=B(a["w_norm"]),
+                   w=B(a["w_gate"]), out=B(a["logits_x"]), layer=int(pend_router.label.split(".")[0][1:]), eps=plan.eps),
+            pend_router.label, [(0, a["input"])])
     # resolve packet sources: the last writer before the stage, else the last writer of the table
     # (previous iteration, negative index); a tensor with no writer gets -1 (never awaited: only the
     # embed's amax when the plan has no head)
@@ -168,6 +188,8 @@ def compile_stages(plan, host):
             outs = {st.aux[6]}
         if st.op == R.FX_OP_GEMV and st.flags & R.FX_F_ARGMAX:
             outs.add(st.aux[3])
+        if st.op == R.FX_OP_MOE_W13 and st.flags & R.FX_F_ROUTER:
+            outs.add(st.aux[0])
         outputs.append(outs)
     for i in range(n):
         for k, name in reads[i]:
@@ -233,13 +255,18 @@ class Runner:
             s0, s1, s2, s3 = (st[i, :, k] for k in range(4))
             ok = s0 > 0
             if not ok.any():
-                rows.append({"label": lab, "start": 0.0, "wait": 0.0, "busy": 0.0, "end": 0.0, "span": 0.0})
+                rows.append({"label": lab, "start": 0.0, "wait": 0.0, "busy": 0.0, "end": 0.0, "span": 0.0, "marks": []})
                 continue
             has_in = ok & (s1 > 0) & (s2 > 0)
             wait = (s1[has_in] - s0[has_in]).max() if has_in.any() else 0.0
             busy = (s2[has_in] - s1[has_in]).max() if has_in.any() else 0.0
+            # op-specific marks 4..7: the median over workers that stamped them, from their input stamp
+            marks = []
+            for k in range(4, 8):
+                m = has_in & (st[i, :, k] > 0)
+                marks.append(float(np.median(st[i, m, k] - s1[m])) if m.any() else None)
             rows.append({"label": lab, "start": s0[ok].min() - t0, "wait": wait, "busy": busy,
-                         "end": s3[ok].max() - t0, "span": s3[ok].max() - s0[ok].min()})
+                         "end": s3[ok].max() - t0, "span": s3[ok].max() - s0[ok].min(), "marks": marks})
         return rows
 
     def timing_us(self):

@@ -143,12 +143,20 @@ def splits_for(s_max, split=SPLIT, n_splits=None):
     return split, n_splits
 
 
-def build_plan(dims: Dims = REAL_DIMS, s_max: int = 1056, layers: int = 27, head: bool = True, split: int = SPLIT,
+def default_splits(s_max):
+    """(split, n_splits) of the decode plan: the fewest 32-position tiles per split that keep every
+    split on its own worker of an XCD (at most 32 splits), so the attention runs in one round and the
+    merge reads at most 32 partials per head."""
+    return splits_for(s_max, n_splits=XWORKERS)
+
+
+def build_plan(dims: Dims = REAL_DIMS, s_max: int = 1056, layers: int = 27, head: bool = True, split: int = None,
                n_splits: int = None, iters_cap: int = 32, softmax_scale: float = SOFTMAX_SCALE,
                eps: float = RMS_EPS) -> Plan:
+    """split / n_splits: the attention split (positions) or split count; neither: default_splits."""
     d = dims
     assert 1 <= layers <= d.L
-    split, n_splits = splits_for(s_max, split, n_splits)
+    split, n_splits = splits_for(s_max, split, n_splits) if (split or n_splits) else default_splits(s_max)
     p = Plan(d, s_max, layers, head, split, n_splits)
     p.scale = softmax_scale
     p.eps = eps

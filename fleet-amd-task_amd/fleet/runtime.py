@@ -21,8 +21,8 @@ FX_OP_GEMV, FX_OP_MLA_PREP, FX_OP_MLA_ATTEND, FX_OP_MLA_MERGE_UV = 1, 2, 3, 4
 FX_OP_MOE_ROUTER, FX_OP_MOE_W13, FX_OP_MOE_W2 = 5, 6, 7
 FX_OP_DENSE_GU, FX_OP_ARGMAX = 9, 10
 FX_IN_VEC, FX_IN_EMBED = 0, 1
-FX_F_NORM, FX_F_RESIDUAL, FX_F_ARGMAX, FX_F_HEAD, FX_F_OUT_LL, FX_F_RES_EMBED = 1, 2, 8, 16, 32, 64
-FX_MAX_ITERS, FX_MAX_MARKS, FX_PROF_SLOTS = 65536, 256, 4
+FX_F_NORM, FX_F_RESIDUAL, FX_F_ARGMAX, FX_F_HEAD, FX_F_OUT_LL, FX_F_RES_EMBED, FX_F_ROUTER = 1, 2, 8, 16, 32, 64, 128
+FX_MAX_ITERS, FX_MAX_MARKS, FX_PROF_SLOTS = 65536, 256, 8
 FX_ABI_VERSION = 3
 WORKERS = 256          # one worker workgroup per CU
 XCDS = 8
@@ -98,6 +98,8 @@ def lib():
         "fx_set_profile": (ctypes.c_int, [vp, i32]),
         "fx_read_profile": (ctypes.c_int, [vp, ctypes.POINTER(ctypes.c_uint64), i32]),
         "fx_run_stage": (ctypes.c_int, [vp, ctypes.POINTER(FxStage), i32, ctypes.c_uint32, i32, vp]),
+        "fx_time_stages": (ctypes.c_int, [vp, ctypes.POINTER(FxStage), i32, i32, i32, ctypes.c_uint32, i32, vp,
+                                          ctypes.POINTER(ctypes.c_float)]),
         "fx_gen_normal_bf16": (ctypes.c_int, [vp, vp, u64, u64, u64, u64, u64, u64, ctypes.c_uint32, ctypes.c_float]),
         "fx_fill_u16": (ctypes.c_int, [vp, vp, u64, ctypes.c_uint16]),
     }
@@ -112,7 +114,7 @@ def lib():
 EXPORTS = ("fx_abi_version", "fx_create", "fx_destroy", "fx_last_error", "fx_device_info", "fx_malloc", "fx_free",
            "fx_memcpy_htod", "fx_memcpy_dtoh", "fx_memcpy_dtod", "fx_memset", "fx_synchronize", "fx_load_plan",
            "fx_run", "fx_launch", "fx_finish", "fx_mark", "fx_marks_ms", "fx_last_run_ms", "fx_set_profile",
-           "fx_read_profile", "fx_read_timing", "fx_run_stage", "fx_gen_normal_bf16", "fx_fill_u16")
+           "fx_read_profile", "fx_read_timing", "fx_run_stage", "fx_time_stages", "fx_gen_normal_bf16", "fx_fill_u16")
 
 
 class Runtime:
@@ -211,6 +213,14 @@ class Runtime:
         """One stage as a standalone launch: packet inputs must carry tbase + src[k] + 1, outputs get
         tbase + sidx + 1."""
         self.check(self.L.fx_run_stage(self.h, ctypes.byref(stage), step, tbase, sidx, None), "fx_run_stage")
+
+    def time_stages(self, stages, reps=10, step=0, tbase=1000, sidx=5):
+        """Mean µs per standalone launch of `stages` launched in turn, `reps` rounds (fx_time_stages)."""
+        arr = (FxStage * len(stages))(*stages)
+        us = ctypes.c_float()
+        self.check(self.L.fx_time_stages(self.h, arr, len(stages), reps, step, tbase, sidx, None, ctypes.byref(us)),
+                   "fx_time_stages")
+        return us.value
 
     def close(self):
         if self.h:

@@ -63,6 +63,15 @@ def report(rows, d, ctx, iter_us=None):
     for k, (cp, bz, n) in sorted(fam.items(), key=lambda kv: -kv[1][0]):
         lines.append(f"| {k} | {n} | {cp:.1f} | {bz:.1f} |")
     lines.append(f"| total | {len(rows)} | {sum(v[0] for v in fam.values()):.1f} | {sum(v[1] for v in fam.values()):.1f} |")
+    marked = [r for r in rows if any(m is not None for m in r.get("marks", []))]
+    if marked:
+        lines += ["", "Operator-internal points (median over workers, µs after the worker's inputs arrived):",
+                  "attention: 4 first tile scored, 5 softmaxed, 6 value product done, 7 partials complete; "
+                  "merge: 4 lse weights, 5 merged o; w13: 4 normed (+ router row), 5 shared slots done, 6 top-k "
+                  "known; w2: 4 shared slots done, 5 routed activations arrived", "", "| stage | 4 | 5 | 6 | 7 |", "|---|---|---|---|---|"]
+        for r in marked[:16]:
+            cells = " | ".join("-" if m is None else f"{m:.2f}" for m in r["marks"])
+            lines.append(f"| {r['label']} | {cells} |")
     if iter_us is not None:
         lines.append(f"\niteration: {iter_us:.1f} us (event clock)")
     return "\n".join(lines)

@@ -27,19 +27,40 @@ def probe_lib():
         raise R.FxError(f"{p} is missing: make -C fleet-amd-task_amd/csrc probe")
     L = ctypes.CDLL(str(p))
     vp, u64, u32 = ctypes.c_void_p, ctypes.c_uint64, ctypes.c_uint32
-    L.fxp_stream.argtypes = [vp, u64, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.POINTER(u64),
+    L.fxp_stream.argtypes = [vp, u64, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.POINTER(u64),
                              ctypes.POINTER(ctypes.c_float)]
     L.fxp_chase.argtypes = [vp, u32, ctypes.c_int, vp, u64, ctypes.c_int, ctypes.POINTER(u64)]
     L.fxp_pingpong.argtypes = [ctypes.c_int, ctypes.c_int, u32, vp, u64, ctypes.c_int, ctypes.POINTER(u64)]
+    L.fxp_lanes.argtypes = [ctypes.POINTER(ctypes.c_float)]
     return L
+
+
+def check_lanes(L):
+    """The DPP / row-swap lane exchange of the butterflies returns lane ^ 2^k for k < 6."""
+    buf = (ctypes.c_float * (64 * 6))()
+    assert L.fxp_lanes(buf) == 0
+    got = np.array(buf, np.float32).reshape(64, 6).astype(np.int64)
+    exp = np.array([[l ^ (1 << k) for k in range(6)] for l in range(64)])
+    bad = np.argwhere(got != exp)
+    return bad, got
 
 
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--out", default=None)
+    ap.add_argument("--lanes-only", action="store_true")
+    ap.add_argument("--stream-only", action="store_true")
     args = ap.parse_args()
     rt = R.Runtime(0)
     L = probe_lib()
+    bad, got = check_lanes(L)
+    print(f"lane exchange: {'ok' if len(bad) == 0 else f'{len(bad)} wrong, first (lane, k) {bad[:4].tolist()}'}",
+          flush=True)
+    if len(bad):
+        print(got[:20], flush=True)
+        sys.exit(1)
+    if args.lanes_only:
+        return
     lines = []
 
     def say(s):
@@ -50,22 +71,31 @@ def main():
     rt.fill_u16(big, 0x3F80, n=big.nbytes // 2)
     rt.synchronize()
     # ---- stream
-    say("## stream: 256 workgroups, GEMV load pattern (each wave: `depth` x 1 KiB loads in flight)\n")
-    say("| threads | depth | KiB/workgroup | GB/s (events) | median µs/wg | max µs/wg |")
-    say("|---|---|---|---|---|---|")
+    say("## stream: 256 workgroups, 1 KiB wave loads (each wave: `depth` loads in flight)\n")
+    say("pattern: contiguous = the wave's loads walk one block in order; gemv = the GEMV tile order (4 rows of "
+        "4 KiB, chunk-major); pairs = the same with two of the rows in the block's second half (gate | up); double-buffered = "
+        "the GEMV pipeline, the next `depth` loads issued before the current ones are consumed\n")
+    say("| threads | depth | pattern | KiB/workgroup | GB/s (events) | median µs/wg | max µs/wg |")
+    say("|---|---|---|---|---|---|---|")
     ticks = (ctypes.c_uint64 * 256)()
     ms = ctypes.c_float()
-    for threads in (256, 512):
-        for depth in (4, 8, 16, 32):
-            for kib in (16, 64, 256, 1024, 4096):
-                if threads == 512 and depth == 32:
-                    continue
-                by = kib * 1024
-                for rep in range(2):
-                    rc = L.fxp_stream(ctypes.c_void_p(big.ptr), by, 256, threads, depth, ticks, ctypes.byref(ms))
-                    assert rc == 0, rc
-                t = np.array(ticks, np.float64) * TICK_NS / 1e3
-                say(f"| {threads} | {depth} | {kib} | {256 * by / (ms.value * 1e-3) / 1e9:.0f} | {np.median(t):.2f} | {t.max():.2f} |")
+    cases = [(256, d, 0, k) for d in (4, 8, 16, 32) for k in (16, 64, 256, 1024, 4096)]
+    cases += [(512, d, 0, k) for d in (4, 8, 16) for k in (64, 256, 1024, 4096)]
+    cases += [(256, d, pat, k) for pat in (1, 2) for d in (16, 32) for k in (64, 256, 1024, 4096)]
+    cases += [(256, d, 3, k) for d in (4, 8, 16) for k in (64, 256, 1024, 4096)]
+    for threads, depth, pat, kib in cases:
+        by = kib * 1024
+        for rep in range(2):
+            rc = L.fxp_stream(ctypes.c_void_p(big.ptr), by, 256, threads, depth, pat, ticks, ctypes.byref(ms))
+            assert rc == 0, rc
+        t = np.array(ticks, np.float64) * TICK_NS / 1e3
+        name = ("contiguous", "gemv", "pairs", "double-buffered")[pat]
+        say(f"| {threads} | {depth} | {name} | {kib} | {256 * by / (ms.value * 1e-3) / 1e9:.0f} | {np.median(t):.2f} | "
+            f"{t.max():.2f} |")
+    if args.stream_only:
+        if args.out:
+            Path(args.out).write_text("\n".join(lines) + "\n")
+        return
     # ---- chase
     say("\n## dependent-load latency (one lane, pointer chase, stride 256 B)\n")
     say("| footprint | policy | load | ns/load |")

@@ -78,12 +78,14 @@ enum fx_op {
   /* [moe_router_layer] h = rmsnorm(x_res(x packets, src[0]), w_norm); logits(out packets f32)[e] =
    * dot(W_gate(w)[e], h) for e < n_rows, row e on worker e. */
   FX_OP_MOE_ROUTER = 5,
-  /* [gang_moe_w13_gemv_layer] softmax/top-k of logits(aux0 packets f32, src[0]); slot x on XCD x
-   * (top-k routed, then the n_forced shared experts E, E+1); h = rmsnorm(x_res(x packets, src[1]));
-   * act8(out packets)[slot][i] = bf16(silu(bf16(W13(w)[e][i] h)) * bf16(W13[e][I+i] h)), I = n_rows.
-   * Worker 0 stores topk_w(aux1 f32), routing(aux2 i32), mask(aux3 i32), logits(aux4 f32), h(aux6)
-   * and route_log(aux5 i32 [prow][aux_i1][n_slots]) at row step - (n_prompt - 1) when that row is in
-   * [0, prow); rank 0 of each XCD stores its slot's expert id to sel(aux7 i32 [8]); aux_i0 = E. */
+  /* [gang_moe_w13_gemv_layer (+ moe_router_layer)] every worker takes pair groups of every slot's
+   * expert (slot s: the top-k routed experts, then the n_forced shared experts E, E+1), shared slots
+   * first; h = rmsnorm(x_res(x packets, src[1])); act8(out packets)[slot][i] = bf16(silu(bf16(W13(w)[e][i] h))
+   * * bf16(W13[e][I+i] h)), I = n_rows; expert ids from logits(aux0 packets f32, src[0]). FX_F_ROUTER:
+   * the stage itself computes logits[e] = dot(W_gate(res)[e], h) on worker e and reads them back.
+   * Worker 0 stores topk_w(aux1 f32), routing(aux2 i32), mask(aux3 i32), logits(aux4 f32), h(aux6),
+   * sel(aux7 i32 [8]) and route_log(aux5 i32 [prow][aux_i1][n_slots]) at row step - (n_prompt - 1) when
+   * that row is in [0, prow); aux_i0 = E. */
   FX_OP_MOE_W13 = 6,
   /* [gang_moe_w2_linear_layer + moe_mul_sum_add_layer] out8[s][n] = bf16(dot(W2(w)[e_s][n],
    * act8(x packets, src[0])[s])) for every slot s, experts from logits(aux0 packets f32, src[1]);
@@ -108,6 +110,7 @@ enum fx_op {
 #define FX_F_HEAD 16u      /* the stage belongs to the head: skipped while step + 1 < n_prompt */
 #define FX_F_OUT_LL 32u    /* output as packets */
 #define FX_F_RES_EMBED 64u /* residual = the embedding row of this iteration's token */
+#define FX_F_ROUTER 128u   /* MOE_W13 computes the router itself (W_gate in res) */
 
 /* One entry of the task table: one operator of the plan (fleet/graph_plan.py Call). */
 typedef struct fx_stage {
@@ -184,9 +187,11 @@ int fx_marks_ms(fx_ctx* ctx, int32_t i, int32_t j, float* ms);
  * gaps, docs/fleet/03-runtime.md:367-371): when iter >= 0, the next fx_run records for iteration
  * `iter` and every worker FX_PROF_SLOTS s_memrealtime stamps per stage, [stage][worker][slot]:
  * slot 0 when the worker begins the stage, slot 1 when its packet inputs have arrived, slot 2
- * when its outputs are issued (0 where a stage has no such point).
+ * when its outputs are issued, slot 3 when it leaves the stage, slots 4..7 at points inside the
+ * operator (attention: scores, softmax and value product of its first tile, partials complete;
+ * merge: lse weights, merged o) -- 0 where a stage has no such point.
  * fx_read_profile copies n_stages * 256 * FX_PROF_SLOTS stamps; returns the count written. */
-#define FX_PROF_SLOTS 4
+#define FX_PROF_SLOTS 8
 int fx_set_profile(fx_ctx* ctx, int32_t iter);
 int fx_read_profile(fx_ctx* ctx, uint64_t* buf, int32_t n);
 
@@ -200,6 +205,13 @@ int fx_read_timing(fx_ctx* ctx, uint64_t* buf, int32_t n);
  * must carry tag tbase + src[k] + 1, outputs get tbase + sidx + 1; the token of an embed residual
  * is tokens(aux4)[step]. */
 int fx_run_stage(fx_ctx* ctx, const fx_stage* stage, int32_t step, uint32_t tbase, int32_t sidx, void* stream);
+
+/* Kernel-suite timing (the reference suite's KT_TIME, fleet/tasks/README.md:294-311): `reps` rounds
+ * of standalone launches of stages[0 .. n) in turn (n copies over different weights defeat the
+ * 256 MB last-level cache), back to back on `stream`; *us = mean microseconds per launch from HIP
+ * events around all of them (launch gaps included). */
+int fx_time_stages(fx_ctx* ctx, const fx_stage* stages, int32_t n, int32_t reps, int32_t step, uint32_t tbase,
+                   int32_t sidx, void* stream, float* us);
 
 /* ---- seeded inputs (pack_weights counterpart: fills the packed keys from a seed) -------------- */
 /* dst[r * dst_stride + j] = bf16(scale * z(src_offset + r * src_stride + j)) for r < rows, j < row_len,

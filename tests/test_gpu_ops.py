@@ -267,6 +267,16 @@ def test_router_experts_combine(rt):
     local = np.arange(9, dtype=np.int32)
     e_act = O.moe_w13_silu(h, W13, local, 8)
     assert mismatch(act8.download(tag=TOUT + 1), e_act) == 0
+    # the same stage with the router folded in (FX_F_ROUTER): logits computed and read back in-stage
+    lxb, act8b = pk_out(rt, (E,), "pk32"), pk_out(rt, (8, I))
+    st.flags = R.FX_F_ROUTER
+    st.res = bufs["W_gate_1"].ptr
+    st.aux[0], st.out = lxb.ptr, act8b.ptr
+    st.src[0] = 0
+    rt.run_stage(st, tbase=TB, sidx=SIDX + 1)
+    assert mismatch(lxb.download(tag=TOUT + 1), logits) == 0
+    assert mismatch(act8b.download(tag=TOUT + 1), e_act) == 0
+    assert np.array_equal(outs["sel"].download(), mask[:8])
     # w2 + combine: act8 (src SIDX + 1), logits (src SIDX), residual x (src SRC); outputs TB + SIDX + 3
     out8 = sentinel(rt, (8, H), "bf16")
     xn = pk_out(rt, (H,))

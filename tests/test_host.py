@@ -41,7 +41,8 @@ def test_plan_counts_and_chain():
     # 1 embed + 27 x (qkva, prep, attend, merge, o_proj) + 2 dense + 26 x 4 MoE calls + 2 head
     assert s["ops"] == 1 + 27 * 5 + 2 + 26 * 4 + 2
     assert p.chain_violations() == []
-    assert (p.split, p.n_splits) == (32, 33)
+    assert (p.split, p.n_splits) == (64, 17)          # default: at most 32 splits (one per XCD worker)
+    assert (G.build_plan(split=32).split, G.build_plan(split=32).n_splits) == (32, 33)
     t = G.build_plan().truncate("L1.o_proj")
     assert t.calls[-1].label == "L1.o_proj"
     assert G.splits_for(32768, n_splits=32) == (1024, 32)
@@ -83,7 +84,7 @@ def test_fold_rules():
     assert stages[0].op == R.FX_OP_GEMV and stages[0].in_kind == R.FX_IN_EMBED
     assert not any("combine" in l for l in labels)
     assert [e.op for e in epi] == [R.FX_OP_ARGMAX]
-    assert n == 7 + 2 * 8 + 1            # layer 0: 7 stages, MoE layers 8 each, head 1
+    assert n == 7 + 2 * 7 + 1            # layer 0: 7 stages, MoE layers 7 each (router in w13), head 1
     # packet sources: the embed's amax is the previous iteration's head; everything else the stage
     # that last wrote the tensor
     assert stages[0].src[1] == -1 and labels[-1] == "head.lm_head"
@@ -93,8 +94,10 @@ def test_fold_rules():
             assert labels[st.src[0]].endswith(".qkva") or labels[st.src[0]].endswith(".qkva+embed")
         if st.op == R.FX_OP_MLA_ATTEND:
             assert ops[st.src[0]] == R.FX_OP_MLA_PREP and st.src[0] == i - 1
+        if st.op == R.FX_OP_MOE_W13:
+            assert st.flags & R.FX_F_ROUTER and labels[i].endswith(".w13+router") and st.res
         if st.op == R.FX_OP_MOE_W2:
-            assert ops[st.src[0]] == R.FX_OP_MOE_W13 and ops[st.src[1]] == R.FX_OP_MOE_ROUTER
+            assert ops[st.src[0]] == R.FX_OP_MOE_W13 and st.src[1] == st.src[0]
             assert labels[st.src[2]].endswith(".o_proj") and st.out == host["x_res"].ptr and st.res == host["x_mid"].ptr
     # layer 0's o_proj takes the embedding row as its residual; later o_projs the x_res packets
     o0 = stages[labels.index("L0.o_proj")]
@@ -107,6 +110,10 @@ def test_fold_rules():
     assert t.calls[-1].label == "L1.combine"
     st, _ = B.compile_stages(t, _fake_host(t))
     assert st[-1].op == R.FX_OP_MOE_W2 and st[0].src[1] == -1
+    # a plan truncated after a router runs it alone
+    t = G.build_plan(layers=3, head=False).truncate("L1.router")
+    st, _ = B.compile_stages(t, _fake_host(t))
+    assert st[-1].op == R.FX_OP_MOE_ROUTER
 
 
 def test_seeded_layout_segments_cover_each_element_once():
