@@ -172,12 +172,17 @@ __device__ __forceinline__ void op_mla_attend(const fx_stage& s, FxEnv& env) {
   void* part = (void*)s.out;
   int done = 0;
   bool have_q = false;
+  // the worker's tiles in order (its splits j = xrank, xrank + 32, .., each in 32-position tiles):
+  // the rows of the next tile are requested as soon as the current one is staged in LDS
+  auto split_hi = [&](int j) { const int h = j * split + split; return h > step + 1 ? step + 1 : h; };
+  u32x4 v[9];
+  if (env.xrank < n_live) {
+    const int lo = env.xrank * split, hi = split_hi(env.xrank);
+    att_issue_rows(v, ckv, kpe, lo, (lo + ATT_T < hi ? lo + ATT_T : hi) - lo, step, d_c, d_r);
+  }
   for (int j = env.xrank; j < n_live; j += env.xworkers) {
     const int lo = j * split;
-    int hi = lo + split;
-    if (hi > step + 1) hi = step + 1;
-    u32x4 v[9];
-    att_issue_rows(v, ckv, kpe, lo, (lo + ATT_T < hi ? lo + ATT_T : hi) - lo, step, d_c, d_r);
+    const int hi = split_hi(j);
     __syncthreads();
     if (!have_q) {
       // q rows of the XCD's heads: ql 2 x 128 pairs (thread t), qp 2 x 16 pairs (threads 0..31)
@@ -213,12 +218,17 @@ __device__ __forceinline__ void op_mla_attend(const fx_stage& s, FxEnv& env) {
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     for (int t0 = lo; t0 < hi; t0 += ATT_T) {
       const int nt = (t0 + ATT_T < hi ? t0 + ATT_T : hi) - t0;
-      if (t0 != lo) att_issue_rows(v, ckv, kpe, t0, nt, step, d_c, d_r);
 #pragma unroll
       for (int k = 0; k < 9; ++k) {
         const int q = threadIdx.x + k * FX_THREADS;
         const int r = q / ATT_CHUNKS, c = q % ATT_CHUNKS;
         if (r < nt && t0 + r != step) *(u32x4*)(tile + r * ATT_ROW + c * 8) = v[k];
+      }
+      {
+        // request the next tile (this split's next 32 positions, or the worker's next split)
+        int nj = j, nt0 = t0 + ATT_T, nhi = hi;
+        if (nt0 >= hi) { nj = j + env.xworkers; nt0 = nj * split; nhi = nj < n_live ? split_hi(nj) : 0; }
+        if (nj < n_live) att_issue_rows(v, ckv, kpe, nt0, (nt0 + ATT_T < nhi ? nt0 + ATT_T : nhi) - nt0, step, d_c, d_r);
       }
       if (step >= t0 && step < t0 + nt && threadIdx.x < (d_c + d_r) / 4) {
         // row `step` from the XCD's packet copy of the cache row

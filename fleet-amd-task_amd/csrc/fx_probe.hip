@@ -208,6 +208,44 @@ __global__ void fxp_lanes_kernel(float* out) {
   out[l * 6 + 5] = xor_lane<32>(v);
 }
 
+// ---- shader clock: block 0 runs a dependent VALU chain of `iters` fmas between two stamps of the
+// core clock (s_memtime) and the 100 MHz real-time clock; the other blocks stream `load` meanwhile
+// (if non-null). out = {core ticks, real ticks, fma chain result bits}
+__global__ void fxp_clock_kernel(int iters, const uint8_t* load, uint64_t load_bytes, uint32_t* done, uint64_t* out) {
+  if (blockIdx.x == 0) {
+    if (threadIdx.x >= 64) return;
+    float a = (float)threadIdx.x, b = 1.0000001f;
+    const uint64_t c0 = __builtin_amdgcn_s_memtime(), r0 = __builtin_amdgcn_s_memrealtime();
+    for (int i = 0; i < iters; ++i) a = __builtin_fmaf(a, b, 1.0f);
+    const uint64_t c1 = __builtin_amdgcn_s_memtime(), r1 = __builtin_amdgcn_s_memrealtime();
+    if (threadIdx.x == 0) {
+      out[0] = c1 - c0;
+      out[1] = r1 - r0;
+      out[2] = __float_as_uint(a);
+      __hip_atomic_store(done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    return;
+  }
+  if (!load) return;
+  const uint64_t per = load_bytes / gridDim.x;
+  const uint8_t* base = load + (uint64_t)blockIdx.x * per;
+  const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+  uint32_t acc = 0;
+  for (int rep = 0; rep < 1000; ++rep) {
+    for (uint64_t off = threadIdx.x * 16; off + 16 * 8 * blockDim.x <= per; off += 16 * 8 * blockDim.x) {
+      u32x4p v[8];
+#pragma unroll
+      for (int d = 0; d < 8; ++d) v[d] = __builtin_nontemporal_load((const u32x4p*)(base + off + (uint64_t)d * 16 * blockDim.x));
+#pragma unroll
+      for (int d = 0; d < 8; ++d) acc += v[d].x;
+    }
+    if (__hip_atomic_load(done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ||
+        __builtin_amdgcn_s_memrealtime() - t0 > PROBE_LIMIT)
+      break;
+  }
+  if (acc == 0x12345678u) out[3] = acc;
+}
+
 extern "C" {
 
 // all functions: 0 on success, else the hipError_t value
@@ -280,6 +318,22 @@ int fxp_lanes(float* out_host) {
   if ((e = hipDeviceSynchronize()) != hipSuccess) return e;
   e = hipMemcpy(out_host, d, 64 * 6 * 4, hipMemcpyDeviceToHost);
   (void)hipFree(d);
+  return e;
+}
+
+int fxp_clock(int iters, const void* load, uint64_t load_bytes, uint64_t* out_host) {
+  uint32_t* done = nullptr;
+  uint64_t* out = nullptr;
+  hipError_t e;
+  if ((e = hipMalloc(&done, 256)) != hipSuccess) return e;
+  if ((e = hipMalloc(&out, 64)) != hipSuccess) return e;
+  (void)hipMemset(done, 0, 256);
+  void* args[] = {&iters, (void*)&load, &load_bytes, &done, &out};
+  if ((e = hipLaunchCooperativeKernel((const void*)fxp_clock_kernel, dim3(256), dim3(256), args, 0, 0)) != hipSuccess) return e;
+  if ((e = hipDeviceSynchronize()) != hipSuccess) return e;
+  e = hipMemcpy(out_host, out, 24, hipMemcpyDeviceToHost);
+  (void)hipFree(done);
+  (void)hipFree(out);
   return e;
 }
 

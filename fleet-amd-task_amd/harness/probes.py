@@ -32,6 +32,7 @@ def probe_lib():
     L.fxp_chase.argtypes = [vp, u32, ctypes.c_int, vp, u64, ctypes.c_int, ctypes.POINTER(u64)]
     L.fxp_pingpong.argtypes = [ctypes.c_int, ctypes.c_int, u32, vp, u64, ctypes.c_int, ctypes.POINTER(u64)]
     L.fxp_lanes.argtypes = [ctypes.POINTER(ctypes.c_float)]
+    L.fxp_clock.argtypes = [ctypes.c_int, vp, u64, ctypes.POINTER(u64)]
     return L
 
 
@@ -50,6 +51,7 @@ def main():
     ap.add_argument("--out", default=None)
     ap.add_argument("--lanes-only", action="store_true")
     ap.add_argument("--stream-only", action="store_true")
+    ap.add_argument("--clock", action="store_true")
     args = ap.parse_args()
     rt = R.Runtime(0)
     L = probe_lib()
@@ -62,6 +64,17 @@ def main():
     if args.lanes_only:
         return
     lines = []
+    if args.clock:
+        big = rt.alloc((2 << 30,), "u8")
+        out = (ctypes.c_uint64 * 3)()
+        for load in (False, True, False):
+            assert L.fxp_clock(2_000_000, ctypes.c_void_p(big.ptr) if load else None, big.nbytes, out) == 0
+            # s_memtime counts the shader clock (core ticks); s_memrealtime 100 MHz
+            mhz = out[0] / (out[1] * 1e-8) / 1e6
+            ns = out[1] * 10.0 / 2_000_000
+            print(f"shader clock {'under stream' if load else 'idle'}: {mhz:.0f} MHz, loop of one dependent fma "
+                  f"+ scalar counter + taken branch: {ns:.2f} ns/iteration ({ns * mhz / 1e3:.1f} core cycles)", flush=True)
+        return
 
     def say(s):
         print(s, flush=True)
