@@ -87,8 +87,58 @@ __device__ void stream_db(const uint8_t* src, uint64_t bytes, uint64_t* ticks, u
   if (acc == 0x12345678u) sink[0] = acc;
 }
 
+// direct-to-LDS walk: each wave owns a ring of D 1 KiB slots in LDS; load d of the wave's block goes
+// to slot d % D via global_load_lds (no VGPRs held), the wave waits until the oldest slot has landed
+// (vmcnt(D - 1)), reads it back with ds_read_b128 and refills the slot with load d + D.
+#define VMCNT(n) (0x0F70 | ((n) & 15) | (((n) >> 4) << 14))
+template <int D>
+__device__ void stream_lds(const uint8_t* src, uint64_t bytes, uint64_t* ticks, uint32_t* sink) {
+  extern __shared__ __attribute__((aligned(16))) char lds_ring[];
+  const uint8_t* base = src + (uint64_t)blockIdx.x * bytes;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  __attribute__((address_space(3))) char* ring = (__attribute__((address_space(3))) char*)lds_ring + wave * D * 1024;
+  const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+  uint32_t acc = 0;
+  // the wave's loads: KiB k = wave, wave + nw, ... of the block
+  const int nk = (int)(bytes >> 10);
+  int issued = 0, k0 = wave;
+  auto issue = [&](int k, int slot) {
+    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(base + (uint64_t)k * 1024 + lane * 16),
+                                     (__attribute__((address_space(3))) void*)(ring + slot * 1024), 16, 0, 0);
+  };
+#pragma unroll
+  for (int d = 0; d < D; ++d) {
+    const int k = wave + d * nw;
+    if (k < nk) issue(k, d);
+  }
+  int d = 0;
+  for (int k = k0; k < nk; k += nw, ++d) {
+    __builtin_amdgcn_s_waitcnt(VMCNT(D - 1));
+    const int slot = d % D;
+    const u32x4p v = *(__attribute__((address_space(3))) u32x4p*)(ring + slot * 1024 + lane * 16);
+    acc += v.x ^ v.y ^ v.z ^ v.w;
+    const int kn = k + D * nw;
+    // the slot is refilled only after its value is in registers
+    __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
+    if (kn < nk) issue(kn, slot);
+    else __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(base + lane * 16),
+                                          (__attribute__((address_space(3))) void*)(ring + slot * 1024), 16, 0, 0);
+  }
+  __builtin_amdgcn_s_waitcnt(VMCNT(0));
+  __syncthreads();
+  if (threadIdx.x == 0) ticks[blockIdx.x] = __builtin_amdgcn_s_memrealtime() - t0;
+  if (acc == 0x12345678u) sink[0] = acc;
+  (void)issued;
+}
+
 __global__ void fxp_stream_kernel(const uint8_t* src, uint64_t bytes, int depth, uint64_t* ticks, uint32_t* sink,
                                   int pattern) {
+  if (pattern == 4) {
+    if (depth == 8) stream_lds<8>(src, bytes, ticks, sink);
+    else if (depth == 16) stream_lds<16>(src, bytes, ticks, sink);
+    else stream_lds<32>(src, bytes, ticks, sink);
+    return;
+  }
   if (pattern == 3) {
     if (depth == 4) stream_db<4>(src, bytes, ticks, sink);
     else if (depth == 8) stream_db<8>(src, bytes, ticks, sink);
@@ -246,6 +296,24 @@ __global__ void fxp_clock_kernel(int iters, const uint8_t* load, uint64_t load_b
   if (acc == 0x12345678u) out[3] = acc;
 }
 
+// ---- direct-to-LDS layout: one wave loads 2 KiB of src (u32 index values) with two 16-byte
+// global_load_lds at LDS offsets 0 and 1024 (the second from src + 1024 + 16 * (63 - lane), lanes
+// reversed), then copies the 2 KiB of LDS to dst as they lie
+__global__ void fxp_lds_dma_kernel(const uint32_t* src, uint32_t* dst) {
+  __shared__ __attribute__((aligned(16))) uint32_t buf[512];
+  const int lane = threadIdx.x;
+  for (int i = lane; i < 512; i += 64) buf[i] = 0xFFFFFFFFu;
+  __syncthreads();
+  __attribute__((address_space(3))) char* l = (__attribute__((address_space(3))) char*)(void*)buf;
+  __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)((const char*)src + lane * 16),
+                                   (__attribute__((address_space(3))) void*)l, 16, 0, 0);
+  __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)((const char*)src + 1024 + (63 - lane) * 16),
+                                   (__attribute__((address_space(3))) void*)(l + 1024), 16, 0, 0);
+  __builtin_amdgcn_s_waitcnt(VMCNT(0));
+  __syncthreads();
+  for (int i = lane; i < 512; i += 64) dst[i] = buf[i];
+}
+
 extern "C" {
 
 // all functions: 0 on success, else the hipError_t value
@@ -260,7 +328,9 @@ int fxp_stream(const void* src, uint64_t bytes_per_block, int blocks, int thread
   (void)hipEventCreate(&e0);
   (void)hipEventCreate(&e1);
   (void)hipEventRecord(e0, 0);
-  hipLaunchKernelGGL(fxp_stream_kernel, dim3(blocks), dim3(threads), 0, 0, (const uint8_t*)src, bytes_per_block, depth,
+  const unsigned shm = pattern == 4 ? (unsigned)(threads / 64) * depth * 1024 : 0;
+  if (shm > 64 * 1024) (void)hipFuncSetAttribute((const void*)fxp_stream_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+  hipLaunchKernelGGL(fxp_stream_kernel, dim3(blocks), dim3(threads), shm, 0, (const uint8_t*)src, bytes_per_block, depth,
                      d_ticks, sink, pattern);
   (void)hipEventRecord(e1, 0);
   if ((e = hipEventSynchronize(e1)) != hipSuccess) return e;
@@ -334,6 +404,22 @@ int fxp_clock(int iters, const void* load, uint64_t load_bytes, uint64_t* out_ho
   e = hipMemcpy(out_host, out, 24, hipMemcpyDeviceToHost);
   (void)hipFree(done);
   (void)hipFree(out);
+  return e;
+}
+
+int fxp_lds_dma(uint32_t* out_host) {
+  uint32_t *src = nullptr, *dst = nullptr;
+  hipError_t e;
+  if ((e = hipMalloc(&src, 2048)) != hipSuccess) return e;
+  if ((e = hipMalloc(&dst, 2048)) != hipSuccess) return e;
+  uint32_t h[512];
+  for (int i = 0; i < 512; ++i) h[i] = (uint32_t)i;
+  if ((e = hipMemcpy(src, h, 2048, hipMemcpyHostToDevice)) != hipSuccess) return e;
+  hipLaunchKernelGGL(fxp_lds_dma_kernel, dim3(1), dim3(64), 0, 0, (const uint32_t*)src, dst);
+  if ((e = hipDeviceSynchronize()) != hipSuccess) return e;
+  e = hipMemcpy(out_host, dst, 2048, hipMemcpyDeviceToHost);
+  (void)hipFree(src);
+  (void)hipFree(dst);
   return e;
 }
 

@@ -33,6 +33,7 @@ def probe_lib():
     L.fxp_pingpong.argtypes = [ctypes.c_int, ctypes.c_int, u32, vp, u64, ctypes.c_int, ctypes.POINTER(u64)]
     L.fxp_lanes.argtypes = [ctypes.POINTER(ctypes.c_float)]
     L.fxp_clock.argtypes = [ctypes.c_int, vp, u64, ctypes.POINTER(u64)]
+    L.fxp_lds_dma.argtypes = [ctypes.POINTER(u32)]
     return L
 
 
@@ -52,6 +53,8 @@ def main():
     ap.add_argument("--lanes-only", action="store_true")
     ap.add_argument("--stream-only", action="store_true")
     ap.add_argument("--clock", action="store_true")
+    ap.add_argument("--reuse", action="store_true",
+                    help="cold (first touch) against warm (re-read) streams, register and direct-to-LDS loads")
     args = ap.parse_args()
     rt = R.Runtime(0)
     L = probe_lib()
@@ -83,6 +86,44 @@ def main():
     big = rt.alloc((2 << 30,), "u8")
     rt.fill_u16(big, 0x3F80, n=big.nbytes // 2)
     rt.synchronize()
+    if args.reuse:
+        # global_load_lds with 16 bytes per lane: lane l's bytes land at the LDS base + 16 l
+        got = (ctypes.c_uint32 * 512)()
+        assert L.fxp_lds_dma(got) == 0
+        g = np.array(got, np.uint32)
+        exp = np.concatenate([np.arange(256), (256 + np.arange(256).reshape(64, 4)[::-1]).reshape(-1)])
+        say(f"direct-to-LDS layout (16 B per lane at base + 16 * lane): {'ok' if (g == exp).all() else 'DIFFERENT'}; "
+            f"first words {g[:8].tolist()}, words 256.. {g[256:264].tolist()}\n")
+        say("## cold and warm streams: 256 workgroups x 256 threads; cold = a region no launch has read since "
+            "1 GiB of other reads, warm = the same region again right after\n")
+        say("| loads | depth | KiB/workgroup | cold median µs/wg | cold max | warm median µs/wg | warm max | "
+            "cold GB/s (max) |")
+        say("|---|---|---|---|---|---|---|---|")
+        ticks = (ctypes.c_uint64 * 256)()
+        ms = ctypes.c_float()
+        half = big.nbytes // 2
+        off = 0
+        for pat, depth in ((0, 8), (3, 8), (4, 16), (4, 32)):
+            for kib in (64, 96, 288, 1024):
+                by = kib * 1024
+                if off + 256 * by > half:
+                    off = 0
+                # flush: stream the second half of the buffer (1 GiB, beyond the last-level cache)
+                assert L.fxp_stream(ctypes.c_void_p(big.ptr + half), half // 256, 256, 256, 8, 0, ticks,
+                                    ctypes.byref(ms)) == 0
+                res = []
+                for rep in range(2):
+                    assert L.fxp_stream(ctypes.c_void_p(big.ptr + off), by, 256, 256, depth, pat, ticks,
+                                        ctypes.byref(ms)) == 0
+                    res.append(np.array(ticks, np.float64) * TICK_NS / 1e3)
+                off += 256 * by
+                c, w = res
+                name = {0: "registers", 3: "registers, double-buffered", 4: "direct to LDS"}[pat]
+                say(f"| {name} | {depth} | {kib} | {np.median(c):.2f} | {c.max():.2f} | {np.median(w):.2f} | "
+                    f"{w.max():.2f} | {256 * by / (c.max() * 1e-6) / 1e9:.0f} |")
+        if args.out:
+            Path(args.out).write_text("\n".join(lines) + "\n")
+        return
     # ---- stream
     say("## stream: 256 workgroups, 1 KiB wave loads (each wave: `depth` loads in flight)\n")
     say("pattern: contiguous = the wave's loads walk one block in order; gemv = the GEMV tile order (4 rows of "
