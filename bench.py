@@ -123,7 +123,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=2, help="untimed decode tokens before the timed ones")
     ap.add_argument("--ctx", type=int, default=1024, help="prompt length (positions attended by the first token)")
     ap.add_argument("--seed", type=int, default=20261201)
-    ap.add_argument("--cpu-tokens", type=int, default=2)
+    ap.add_argument("--cpu-tokens", type=int, default=16)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--n-splits", type=int, default=None, help="attention splits (default: 32-position splits)")
     args = ap.parse_args()
