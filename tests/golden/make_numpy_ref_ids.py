@@ -1,4 +1,5 @@
-"""Writes numpy_ref_decode.json: greedy ids, route ids and the final hidden row of a short decode
+"""Writes numpy_ref_decode.json: greedy ids, route ids, the hidden row after every layer of every
+decode step and the final hidden row of a short decode
 computed by the reference's own numpy operators (harness/numpy_ref.py), composed in the
 reference's task-graph order (fleet/graph_plan.py:380-603), on the seeded synthetic weights.
 
@@ -66,10 +67,12 @@ def main():
     c_kv = [np.zeros((S_MAX, c.D_C), np.float32) for _ in range(LAYERS)]
     k_pe = [np.zeros((S_MAX, c.D_R), np.float32) for _ in range(LAYERS)]
 
-    def step_fn(token, step, head):
+    def step_fn(token, step, head, hidden=None):
         x = w("W_embed")[token].copy()
         routes = []
         for l in range(LAYERS):
+            if hidden is not None and l > 0:
+                hidden.append([int(v) for v in O.f32_to_bf16(x)])
             _, qkva = nr.linear_norm(x, w(f"w_norm1_{l}"), w(f"W_qkva_{l}"), eps=c.eps)
             c_row, k_row, ql, qp = nr.mla_prep(qkva, w(f"w_kv_norm_{l}"), w(f"W_uk_{l}"), cos[step], sin[step],
                                                nh=c.NH, d_n=c.D_N, d_r=c.D_R, d_c=c.D_C, eps=c.eps)
@@ -101,6 +104,8 @@ def main():
             srt = np.sort(logits)[::-1]
             routes.append({"ids": ids, "logits": [float(logits[e]) for e in ids[:c.TOPK]],
                            "gap_6_7": float(srt[c.TOPK - 1] - srt[c.TOPK])})
+        if hidden is not None:
+            hidden.append([int(v) for v in O.f32_to_bf16(x)])
         if not head:
             return None, routes, x
         _, logits = nr.linear_norm(x, w("w_final_norm"), w("W_lm"), eps=c.eps)
@@ -115,8 +120,10 @@ def main():
     x = None
     for i in range(N_NEW):
         step = N_PROMPT - 1 + i
-        t, routes, x = step_fn(tok, step, True)
-        steps.append({"step": step, "token": t["id"], "logit_gap_1_2": t["gap_1_2"], "routes": routes})
+        hidden = []
+        t, routes, x = step_fn(tok, step, True, hidden)
+        steps.append({"step": step, "token": t["id"], "logit_gap_1_2": t["gap_1_2"], "routes": routes,
+                      "hidden_bf16": hidden})
         tok = t["id"]
     out = {
         "what": "greedy decode by harness/numpy_ref.py operators on seeded synthetic weights",

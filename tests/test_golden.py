@@ -74,3 +74,29 @@ def test_final_hidden_row_within_bf16_drift(decoded):
     assert rel < 0.02, rel
     # a dropped residual or a transposed operand moves the row by O(1), not O(1e-2)
     assert np.corrcoef(ours, ref)[0, 1] > 0.999
+
+
+def hidden_errors(g, out):
+    """(step, layer, max_abs, rel) of the oracle's hidden row after each layer against numpy_ref's."""
+    rows = []
+    for (_, _, rec), st in zip(out, g["steps"]):
+        for l, ref_bits in enumerate(st["hidden_bf16"]):
+            ref = O.bf16_to_f32(np.array(ref_bits, np.uint16))
+            ours = O.bf16_to_f32(np.asarray(rec[f"L{l}.B13.layer_out"]))
+            d = ours - ref
+            rows.append((st["step"], l, float(np.abs(d).max()), float(np.linalg.norm(d) / np.linalg.norm(ref))))
+    return rows
+
+
+def test_per_layer_hidden_rows_within_bf16_tolerance(decoded):
+    """Every decode step's hidden row after each layer, oracle (= GPU, bit for bit) against
+    numpy_ref: FP32 accumulation in both, bf16 storage. Tolerance: rel (L2 norm of the difference
+    over the reference's) < 1e-2 and max-abs at most 4 bf16 ulps of the row's largest element;
+    measured on this fixture (8 rows): rel 4.1e-3 .. 7.2e-3, max-abs 1 .. 2 ulps."""
+    g, out, _ = decoded
+    for step, l, max_abs, rel in hidden_errors(g, out):
+        ref_max = float(np.abs(O.bf16_to_f32(np.array(g["steps"][step - g["steps"][0]["step"]]["hidden_bf16"][l],
+                                                       np.uint16))).max())
+        ulp = 2.0 ** (np.floor(np.log2(ref_max)) - 7)
+        assert rel < 1e-2, (step, l, rel)
+        assert max_abs <= 4 * ulp, (step, l, max_abs, ulp)
