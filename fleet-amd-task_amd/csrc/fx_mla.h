@@ -137,12 +137,22 @@ __device__ __forceinline__ void op_mla_prep(const fx_stage& s, FxEnv& env) {
 #define ATT_ROW 584   // bf16 elements per staged row: 576 + 8 pad (1168 bytes: conflict-free b128 reads)
 #define ATT_CHUNKS 72 // 16-byte chunks of one position: 64 latent + 8 rope
 
+// LDS of the attention stage: a pass stages up to two consecutive tiles of one split (64 rows of
+// ATT_ROW), then q and the per-pass scratch
+#define ATT_PASS (2 * ATT_T)
+#define ATT_Q_OFF (ATT_PASS * ATT_ROW * 2)                     // 74752
+#define ATT_SP_OFF (ATT_Q_OFF + (MLA_HP * 512 + MLA_HP * 64) * 4)
+#define ATT_PB_OFF (ATT_SP_OFF + 2 * MLA_HP * ATT_T * 5 * 4)
+#define ATT_HS_OFF (ATT_PB_OFF + 2 * MLA_HP * ATT_T * 4)
+static_assert(ATT_HS_OFF + MLA_HP * 4 * 4 <= LDS_STAGE, "attention LDS overlaps the stage descriptor");
+#define ATT_LOADS ((ATT_PASS * ATT_CHUNKS + FX_THREADS - 1) / FX_THREADS)   // 18 16-byte loads per thread
+
+// rows t0 .. t0 + nt - 1 (nt <= 64) below `step` into registers (row `step` and later rows are never
+// read from the caches: a line loaded before it is written could stay stale in this XCD's caches)
 __device__ __forceinline__ void att_issue_rows(u32x4* v, const uint16_t* ckv, const uint16_t* kpe, int t0, int nt,
                                                int step, int d_c, int d_r) {
-  // rows t0 .. t0 + nt - 1 below `step` (row `step` and later rows are never read from the caches:
-  // a line loaded before it is written could stay stale in this XCD's caches)
 #pragma unroll
-  for (int k = 0; k < 9; ++k) {
+  for (int k = 0; k < ATT_LOADS; ++k) {
     const int q = threadIdx.x + k * FX_THREADS;
     const int r = q / ATT_CHUNKS, c = q % ATT_CHUNKS;
     int rr = t0 + (r < nt ? r : 0);
@@ -152,6 +162,9 @@ __device__ __forceinline__ void att_issue_rows(u32x4* v, const uint16_t* ckv, co
   }
 }
 
+// FX_OP_MLA_ATTEND. A worker walks its splits j = xrank, xrank + 32, .. in passes of up to two
+// consecutive 32-position tiles: the scores and value products of the two tiles are computed side by
+// side (independent chains), the online softmax still advances tile by tile in position order.
 __device__ __forceinline__ void op_mla_attend(const fx_stage& s, FxEnv& env) {
   const int nh = s.n_rows, d_c = s.d_c, d_r = s.d_r, prow = s.prow;
   const int h0 = env.xcd * MLA_HP;
@@ -160,26 +173,28 @@ __device__ __forceinline__ void op_mla_attend(const fx_stage& s, FxEnv& env) {
   const int n_live = (step + 1 + split - 1) / split;
   const float scale = s.scale;
   const uint32_t tin = tag_in(s, env, 0);
-  float* ql = (float*)(env.lds + LDS_XS);                 // [2][512]
-  float* qp = ql + 2 * 512;                               // [2][64]
-  float* sp = qp + 2 * 64;                                // [2][32][5] partial scores
-  float* pb = sp + 2 * 32 * 5;                            // [2][32] bf16(p)
-  float* hs = pb + 64;                                    // [2][4] m, l, alpha
-  uint16_t* tile = (uint16_t*)(env.lds + LDS_TILE);       // [32][ATT_ROW]
+  uint16_t* buf = (uint16_t*)env.lds;                            // [64][ATT_ROW]
+  float* ql = (float*)(env.lds + ATT_Q_OFF);                     // [2][512]
+  float* qp = ql + MLA_HP * 512;                                 // [2][64]
+  float* sp = (float*)(env.lds + ATT_SP_OFF);                    // [2 tiles][2 heads][32][5] partial scores
+  float* pb = (float*)(env.lds + ATT_PB_OFF);                    // [2 tiles][2 heads][32] bf16(p)
+  float* hs = (float*)(env.lds + ATT_HS_OFF);                    // [2 heads][4]: m, l, alpha A, alpha B
   const uint16_t* ckv = (const uint16_t*)s.aux[0];
   const uint16_t* kpe = (const uint16_t*)s.aux[1];
   const void* crow = (const uint8_t*)s.aux[5] + (size_t)env.xcd * (d_c + d_r) / 2 * 8;
   void* part = (void*)s.out;
   int done = 0;
   bool have_q = false;
-  // the worker's tiles in order (its splits j = xrank, xrank + 32, .., each in 32-position tiles):
-  // the rows of the next tile are requested as soon as the current one is staged in LDS
   auto split_hi = [&](int j) { const int h = j * split + split; return h > step + 1 ? step + 1 : h; };
-  u32x4 v[9];
+  auto pass_rows = [&](int t0, int hi) { return (t0 + ATT_PASS < hi ? t0 + ATT_PASS : hi) - t0; };
+  // the rows of the next pass are requested as soon as the current pass is staged in LDS
+  u32x4 v[ATT_LOADS];
   if (env.xrank < n_live) {
-    const int lo = env.xrank * split, hi = split_hi(env.xrank);
-    att_issue_rows(v, ckv, kpe, lo, (lo + ATT_T < hi ? lo + ATT_T : hi) - lo, step, d_c, d_r);
+    const int lo = env.xrank * split;
+    att_issue_rows(v, ckv, kpe, lo, pass_rows(lo, split_hi(env.xrank)), step, d_c, d_r);
   }
+  // online-softmax state of the running split (wave 0, lane (h, t): identical on a head's 32 lanes)
+  float m_run = -__builtin_inff(), l_run = 0.0f;
   for (int j = env.xrank; j < n_live; j += env.xworkers) {
     const int lo = j * split;
     const int hi = split_hi(j);
@@ -212,143 +227,193 @@ __device__ __forceinline__ void op_mla_attend(const fx_stage& s, FxEnv& env) {
       have_q = true;
       prof_mark(env, 1);
     }
-    if (threadIdx.x < MLA_HP) { hs[threadIdx.x * 4 + 0] = -__builtin_inff(); hs[threadIdx.x * 4 + 1] = 0.0f; }
+    m_run = -__builtin_inff();
+    l_run = 0.0f;
     // accumulators: thread -> head ph = tid >> 7, columns pc .. pc + 3
     const int ph = threadIdx.x >> 7, pc = (threadIdx.x & 127) * 4;
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int t0 = lo; t0 < hi; t0 += ATT_T) {
-      const int nt = (t0 + ATT_T < hi ? t0 + ATT_T : hi) - t0;
+    for (int t0 = lo; t0 < hi; t0 += ATT_PASS) {
+      const int nt = pass_rows(t0, hi);
+      const int ntA = nt < ATT_T ? nt : ATT_T, ntB = nt - ntA;
 #pragma unroll
-      for (int k = 0; k < 9; ++k) {
+      for (int k = 0; k < ATT_LOADS; ++k) {
         const int q = threadIdx.x + k * FX_THREADS;
         const int r = q / ATT_CHUNKS, c = q % ATT_CHUNKS;
-        if (r < nt && t0 + r != step) *(u32x4*)(tile + r * ATT_ROW + c * 8) = v[k];
+        if (r < nt && t0 + r != step) *(u32x4*)(buf + r * ATT_ROW + c * 8) = v[k];
       }
       {
-        // request the next tile (this split's next 32 positions, or the worker's next split)
-        int nj = j, nt0 = t0 + ATT_T, nhi = hi;
+        // request the next pass (this split's next 64 positions, or the worker's next split)
+        int nj = j, nt0 = t0 + ATT_PASS, nhi = hi;
         if (nt0 >= hi) { nj = j + env.xworkers; nt0 = nj * split; nhi = nj < n_live ? split_hi(nj) : 0; }
-        if (nj < n_live) att_issue_rows(v, ckv, kpe, nt0, (nt0 + ATT_T < nhi ? nt0 + ATT_T : nhi) - nt0, step, d_c, d_r);
+        if (nj < n_live) att_issue_rows(v, ckv, kpe, nt0, pass_rows(nt0, nhi), step, d_c, d_r);
       }
       if (step >= t0 && step < t0 + nt && threadIdx.x < (d_c + d_r) / 4) {
         // row `step` from the XCD's packet copy of the cache row
         u32x4 w[1];
         pk_wait_pairs<1>(crow, threadIdx.x, 0, threadIdx.x + 1, tin, env.err, w);
-        uint32_t* dst = (uint32_t*)(tile + (step - t0) * ATT_ROW) + 2 * threadIdx.x;
+        uint32_t* dst = (uint32_t*)(buf + (step - t0) * ATT_ROW) + 2 * threadIdx.x;
         dst[0] = w[0].x;
         dst[1] = w[0].z;
       }
       __syncthreads();
-      // scores: thread (h, k, t): chain k over latent columns [128k, 128k + 128); k == 0 also the
-      // rope chain; s = ((((n0 + n1) + n2) + n3) + pe) * scale. Consecutive lanes take consecutive
-      // rows t (row stride 1168 B = 16 B mod 128: conflict-free b128 reads) and share q (broadcast).
+      // scores: thread (h, k, t): chain k over latent columns [128k, 128k + 128) of row t of tile A
+      // and of tile B side by side; k == 0 also the rope chains; s = ((((n0 + n1) + n2) + n3) + pe)
+      // * scale. Consecutive lanes take consecutive rows (row stride 1168 B: conflict-free b128
+      // reads) and share q (broadcast). A missing tile-B row is computed on stale data and dropped.
       {
         const int h = threadIdx.x >> 7, k = (threadIdx.x >> 5) & 3, t = threadIdx.x & 31;
-        float a = 0.0f, b = 0.0f;
-        if (t < nt) {
-          const uint16_t* kr = tile + t * ATT_ROW;
-          const float* qr = ql + h * 512;
+        float a = 0.0f, a2 = 0.0f, b = 0.0f, b2 = 0.0f;
+        const uint16_t* kr = buf + t * ATT_ROW;
+        const uint16_t* kr2 = buf + (ATT_T + t) * ATT_ROW;
+        const float* qr = ql + h * 512;
+        if (t < ntA) {
 #pragma unroll 4
           for (int c = k * 128; c < k * 128 + 128; c += 8) {
             const u32x4 kv = *(const u32x4*)(kr + c);
+            const u32x4 kv2 = *(const u32x4*)(kr2 + c);
             const float4 q0 = *(const float4*)(qr + c), q1 = *(const float4*)(qr + c + 4);
             a = __builtin_fmaf(q0.x, bf_lo(kv.x), a);
+            a2 = __builtin_fmaf(q0.x, bf_lo(kv2.x), a2);
             a = __builtin_fmaf(q0.y, bf_hi(kv.x), a);
+            a2 = __builtin_fmaf(q0.y, bf_hi(kv2.x), a2);
             a = __builtin_fmaf(q0.z, bf_lo(kv.y), a);
+            a2 = __builtin_fmaf(q0.z, bf_lo(kv2.y), a2);
             a = __builtin_fmaf(q0.w, bf_hi(kv.y), a);
+            a2 = __builtin_fmaf(q0.w, bf_hi(kv2.y), a2);
             a = __builtin_fmaf(q1.x, bf_lo(kv.z), a);
+            a2 = __builtin_fmaf(q1.x, bf_lo(kv2.z), a2);
             a = __builtin_fmaf(q1.y, bf_hi(kv.z), a);
+            a2 = __builtin_fmaf(q1.y, bf_hi(kv2.z), a2);
             a = __builtin_fmaf(q1.z, bf_lo(kv.w), a);
+            a2 = __builtin_fmaf(q1.z, bf_lo(kv2.w), a2);
             a = __builtin_fmaf(q1.w, bf_hi(kv.w), a);
+            a2 = __builtin_fmaf(q1.w, bf_hi(kv2.w), a2);
           }
           if (k == 0) {
             const float* qpr = qp + h * 64;
 #pragma unroll
             for (int r = 0; r < 64; r += 8) {
               const u32x4 kv = *(const u32x4*)(kr + 512 + r);
-              b = __builtin_fmaf(qpr[r + 0], bf_lo(kv.x), b);
-              b = __builtin_fmaf(qpr[r + 1], bf_hi(kv.x), b);
-              b = __builtin_fmaf(qpr[r + 2], bf_lo(kv.y), b);
-              b = __builtin_fmaf(qpr[r + 3], bf_hi(kv.y), b);
-              b = __builtin_fmaf(qpr[r + 4], bf_lo(kv.z), b);
-              b = __builtin_fmaf(qpr[r + 5], bf_hi(kv.z), b);
-              b = __builtin_fmaf(qpr[r + 6], bf_lo(kv.w), b);
-              b = __builtin_fmaf(qpr[r + 7], bf_hi(kv.w), b);
+              const u32x4 kv2 = *(const u32x4*)(kr2 + 512 + r);
+              const float4 q0 = *(const float4*)(qpr + r), q1 = *(const float4*)(qpr + r + 4);
+              b = __builtin_fmaf(q0.x, bf_lo(kv.x), b);
+              b2 = __builtin_fmaf(q0.x, bf_lo(kv2.x), b2);
+              b = __builtin_fmaf(q0.y, bf_hi(kv.x), b);
+              b2 = __builtin_fmaf(q0.y, bf_hi(kv2.x), b2);
+              b = __builtin_fmaf(q0.z, bf_lo(kv.y), b);
+              b2 = __builtin_fmaf(q0.z, bf_lo(kv2.y), b2);
+              b = __builtin_fmaf(q0.w, bf_hi(kv.y), b);
+              b2 = __builtin_fmaf(q0.w, bf_hi(kv2.y), b2);
+              b = __builtin_fmaf(q1.x, bf_lo(kv.z), b);
+              b2 = __builtin_fmaf(q1.x, bf_lo(kv2.z), b2);
+              b = __builtin_fmaf(q1.y, bf_hi(kv.z), b);
+              b2 = __builtin_fmaf(q1.y, bf_hi(kv2.z), b2);
+              b = __builtin_fmaf(q1.z, bf_lo(kv.w), b);
+              b2 = __builtin_fmaf(q1.z, bf_lo(kv2.w), b2);
+              b = __builtin_fmaf(q1.w, bf_hi(kv.w), b);
+              b2 = __builtin_fmaf(q1.w, bf_hi(kv2.w), b2);
             }
           }
         }
-        sp[(h * 32 + t) * 5 + k] = a;
-        if (k == 0) sp[(h * 32 + t) * 5 + 4] = b;
+        float* spA = sp + (h * ATT_T + t) * 5;
+        float* spB = sp + ((MLA_HP + h) * ATT_T + t) * 5;
+        spA[k] = a;
+        spB[k] = a2;
+        if (k == 0) { spA[4] = b; spB[4] = b2; }
       }
       __syncthreads();
       if (done == 0 && t0 == lo) prof_mark(env, 4);
-      // softmax of the tile on wave 0 (lane = h * 32 + t); the sum of p runs sequentially in t
-      // (lane by lane through scalar reads), then l = l * alpha + psum
+      // softmax on wave 0 (lane = h * 32 + t), tile A then tile B: m_new = max(m, max_t s),
+      // alpha = exp(m - m_new), p = exp(s - m_new); the sum of p runs sequentially in t (lane by
+      // lane through scalar reads); l = l * alpha + psum
       if (threadIdx.x < 64) {
         const int h = threadIdx.x >> 5, t = threadIdx.x & 31;
-        float sc = -__builtin_inff();
-        if (t < nt) {
-          const float* q = sp + (h * 32 + t) * 5;
-          float v2 = q[0] + q[1];
-          v2 = v2 + q[2];
-          v2 = v2 + q[3];
-          v2 = v2 + q[4];
-          sc = v2 * scale;
-        }
-        float mt = sc;
-        mt = fmaxf(mt, xor_lane<1>(mt));
-        mt = fmaxf(mt, xor_lane<2>(mt));
-        mt = fmaxf(mt, xor_lane<4>(mt));
-        mt = fmaxf(mt, xor_lane<8>(mt));
-        mt = fmaxf(mt, xor_lane<16>(mt));
-        const float m = hs[h * 4 + 0];
-        const float m_new = m > mt ? m : mt;
-        const float alpha = exp_s(m - m_new);
-        const float p = t < nt ? exp_s(sc - m_new) : 0.0f;
-        pb[h * 32 + t] = bf16r(p);
-        float ps0 = 0.0f, ps1 = 0.0f;
+        for (int tile = 0; tile < 2; ++tile) {
+          const int ntt = tile ? ntB : ntA;
+          if (ntt <= 0) break;
+          float sc = -__builtin_inff();
+          if (t < ntt) {
+            const float* q = sp + ((tile * MLA_HP + h) * ATT_T + t) * 5;
+            float v2 = q[0] + q[1];
+            v2 = v2 + q[2];
+            v2 = v2 + q[3];
+            v2 = v2 + q[4];
+            sc = v2 * scale;
+          }
+          float mt = sc;
+          mt = fmaxf(mt, xor_lane<1>(mt));
+          mt = fmaxf(mt, xor_lane<2>(mt));
+          mt = fmaxf(mt, xor_lane<4>(mt));
+          mt = fmaxf(mt, xor_lane<8>(mt));
+          mt = fmaxf(mt, xor_lane<16>(mt));
+          const float m_new = m_run > mt ? m_run : mt;
+          const float alpha = exp_s(m_run - m_new);
+          const float p = t < ntt ? exp_s(sc - m_new) : 0.0f;
+          pb[(tile * MLA_HP + h) * ATT_T + t] = bf16r(p);
+          float ps0 = 0.0f, ps1 = 0.0f;
 #pragma unroll
-        for (int u = 0; u < 32; ++u) {
-          ps0 = ps0 + __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, p), u));
-          ps1 = ps1 + __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, p), 32 + u));
-        }
-        if (t == 0) {
-          const float l = hs[h * 4 + 1];
-          hs[h * 4 + 1] = l * alpha + (h ? ps1 : ps0);
-          hs[h * 4 + 2] = alpha;
-          hs[h * 4 + 0] = m_new;
+          for (int u = 0; u < 32; ++u) {
+            ps0 = ps0 + __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, p), u));
+            ps1 = ps1 + __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, p), 32 + u));
+          }
+          l_run = l_run * alpha + (h ? ps1 : ps0);
+          m_run = m_new;
+          if (t == 0) {
+            hs[h * 4 + 2 + tile] = alpha;
+            hs[h * 4 + 0] = m_run;
+            hs[h * 4 + 1] = l_run;
+          }
         }
       }
       __syncthreads();
       if (done == 0 && t0 == lo) prof_mark(env, 5);
-      // value product over the tile, sequential in t: tp[c] = sum_t bf16(p_t) v_t[c];
-      // acc = acc * alpha + tp
+      // value products, tile A and tile B side by side, each sequential in t:
+      // tp[c] = sum_t bf16(p_t) v_t[c]; acc = acc * alpha_A + tp_A, then acc * alpha_B + tp_B
       {
-        const float alpha = hs[ph * 4 + 2];
-        float tp[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        // 8 rows' loads at a time, then their fmas in t order (rows past nt carry p = 0 and are
-        // skipped: their tile rows are stale)
-        for (int t8 = 0; t8 < nt; t8 += 8) {
-          u32x2 kv[8];
-          float pv[8];
+        float tp[4] = {0.0f, 0.0f, 0.0f, 0.0f}, tq[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        const float* pA = pb + ph * ATT_T;
+        const float* pB = pb + (MLA_HP + ph) * ATT_T;
+        // 8 rows of each tile loaded at a time, then their fmas in t order (rows past a tile's end
+        // carry p = 0 and are skipped: their staged rows are stale)
+        for (int t8 = 0; t8 < ntA; t8 += 8) {
+          u32x2 kv[8], kv2[8];
+          float pv[8], pv2[8];
 #pragma unroll
           for (int u = 0; u < 8; ++u) {
-            kv[u] = *(const u32x2*)(tile + (t8 + u) * ATT_ROW + pc);
-            pv[u] = pb[ph * 32 + t8 + u];
+            kv[u] = *(const u32x2*)(buf + (t8 + u) * ATT_ROW + pc);
+            kv2[u] = *(const u32x2*)(buf + (ATT_T + t8 + u) * ATT_ROW + pc);
+            pv[u] = pA[t8 + u];
+            pv2[u] = pB[t8 + u];
           }
 #pragma unroll
           for (int u = 0; u < 8; ++u) {
-            if (t8 + u >= nt) break;
-            tp[0] = __builtin_fmaf(pv[u], bf_lo(kv[u].x), tp[0]);
-            tp[1] = __builtin_fmaf(pv[u], bf_hi(kv[u].x), tp[1]);
-            tp[2] = __builtin_fmaf(pv[u], bf_lo(kv[u].y), tp[2]);
-            tp[3] = __builtin_fmaf(pv[u], bf_hi(kv[u].y), tp[3]);
+            if (t8 + u < ntA) {
+              tp[0] = __builtin_fmaf(pv[u], bf_lo(kv[u].x), tp[0]);
+              tp[1] = __builtin_fmaf(pv[u], bf_hi(kv[u].x), tp[1]);
+              tp[2] = __builtin_fmaf(pv[u], bf_lo(kv[u].y), tp[2]);
+              tp[3] = __builtin_fmaf(pv[u], bf_hi(kv[u].y), tp[3]);
+            }
+            if (t8 + u < ntB) {
+              tq[0] = __builtin_fmaf(pv2[u], bf_lo(kv2[u].x), tq[0]);
+              tq[1] = __builtin_fmaf(pv2[u], bf_hi(kv2[u].x), tq[1]);
+              tq[2] = __builtin_fmaf(pv2[u], bf_lo(kv2[u].y), tq[2]);
+              tq[3] = __builtin_fmaf(pv2[u], bf_hi(kv2[u].y), tq[3]);
+            }
           }
         }
+        const float alphaA = hs[ph * 4 + 2];
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
-          const float a = acc[c] * alpha;
+          const float a = acc[c] * alphaA;
           acc[c] = a + tp[c];
+        }
+        if (ntB > 0) {
+          const float alphaB = hs[ph * 4 + 3];
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            const float a = acc[c] * alphaB;
+            acc[c] = a + tq[c];
+          }
         }
       }
       __syncthreads();
