@@ -144,7 +144,7 @@ __device__ __forceinline__ void op_mla_prep(const fx_stage& s, FxEnv& env) {
 #define ATT_SP_OFF (ATT_Q_OFF + (MLA_HP * 512 + MLA_HP * 64) * 4)
 #define ATT_PB_OFF (ATT_SP_OFF + 2 * MLA_HP * ATT_T * 5 * 4)
 #define ATT_HS_OFF (ATT_PB_OFF + 2 * MLA_HP * ATT_T * 4)
-static_assert(ATT_HS_OFF + MLA_HP * 4 * 4 <= LDS_STAGE, "attention LDS overlaps the stage descriptor");
+static_assert(ATT_HS_OFF + MLA_HP * 5 * 4 <= LDS_STAGE, "attention LDS overlaps the stage descriptor");
 #define ATT_LOADS ((ATT_PASS * ATT_CHUNKS + FX_THREADS - 1) / FX_THREADS)   // 18 16-byte loads per thread
 
 // rows t0 .. t0 + nt - 1 (nt <= 64) below `step` into registers (row `step` and later rows are never
@@ -179,6 +179,7 @@ __device__ __forceinline__ void op_mla_attend(const fx_stage& s, FxEnv& env) {
   float* sp = (float*)(env.lds + ATT_SP_OFF);                    // [2 tiles][2 heads][32][5] partial scores
   float* pb = (float*)(env.lds + ATT_PB_OFF);                    // [2 tiles][2 heads][32] bf16(p)
   float* hs = (float*)(env.lds + ATT_HS_OFF);                    // [2 heads][4]: m, l, alpha A, alpha B
+  float* psB = hs + MLA_HP * 4;                                  // [2 heads] tile B's sum of p
   const uint16_t* ckv = (const uint16_t*)s.aux[0];
   const uint16_t* kpe = (const uint16_t*)s.aux[1];
   const void* crow = (const uint8_t*)s.aux[5] + (size_t)env.xcd * (d_c + d_r) / 2 * 8;
@@ -323,61 +324,80 @@ __device__ __forceinline__ void op_mla_attend(const fx_stage& s, FxEnv& env) {
       }
       __syncthreads();
       if (done == 0 && t0 == lo) prof_mark(env, 4);
-      // softmax on wave 0 (lane = h * 32 + t), tile A then tile B: m_new = max(m, max_t s),
-      // alpha = exp(m - m_new), p = exp(s - m_new); the sum of p runs sequentially in t (lane by
-      // lane through scalar reads); l = l * alpha + psum
-      if (threadIdx.x < 64) {
-        const int h = threadIdx.x >> 5, t = threadIdx.x & 31;
-        for (int tile = 0; tile < 2; ++tile) {
-          const int ntt = tile ? ntB : ntA;
-          if (ntt <= 0) break;
+      // softmax, tile A on wave 0 and tile B on wave 1 (lane = h * 32 + t): m_A = max(m, max_t s_A),
+      // m_B = max(m_A, max_t s_B), alpha = exp(m_prev - m_new), p = exp(s - m_new); each tile's sum
+      // of p runs sequentially in t (lane by lane through scalar reads). The running (m, l) stays on
+      // wave 0: l = (l * alpha_A + psum_A) * alpha_B + psum_B, the tile order of the spec.
+      if (threadIdx.x < 64 || (threadIdx.x < 128 && ntB > 0)) {
+        const int tile = threadIdx.x >> 6;
+        const int h = (threadIdx.x >> 5) & 1, t = threadIdx.x & 31;
+        auto tile_score = [&](int tl, int ntt) {
           float sc = -__builtin_inff();
           if (t < ntt) {
-            const float* q = sp + ((tile * MLA_HP + h) * ATT_T + t) * 5;
+            const float* q = sp + ((tl * MLA_HP + h) * ATT_T + t) * 5;
             float v2 = q[0] + q[1];
             v2 = v2 + q[2];
             v2 = v2 + q[3];
             v2 = v2 + q[4];
             sc = v2 * scale;
           }
-          float mt = sc;
-          mt = fmaxf(mt, xor_lane<1>(mt));
-          mt = fmaxf(mt, xor_lane<2>(mt));
-          mt = fmaxf(mt, xor_lane<4>(mt));
-          mt = fmaxf(mt, xor_lane<8>(mt));
-          mt = fmaxf(mt, xor_lane<16>(mt));
-          const float m_new = m_run > mt ? m_run : mt;
-          const float alpha = exp_s(m_run - m_new);
-          const float p = t < ntt ? exp_s(sc - m_new) : 0.0f;
-          pb[(tile * MLA_HP + h) * ATT_T + t] = bf16r(p);
-          float ps0 = 0.0f, ps1 = 0.0f;
-#pragma unroll
-          for (int u = 0; u < 32; ++u) {
-            ps0 = ps0 + __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, p), u));
-            ps1 = ps1 + __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, p), 32 + u));
-          }
-          l_run = l_run * alpha + (h ? ps1 : ps0);
-          m_run = m_new;
-          if (t == 0) {
-            hs[h * 4 + 2 + tile] = alpha;
-            hs[h * 4 + 0] = m_run;
-            hs[h * 4 + 1] = l_run;
-          }
+          return sc;
+        };
+        auto max32 = [&](float x) {
+          x = fmaxf(x, xor_lane<1>(x));
+          x = fmaxf(x, xor_lane<2>(x));
+          x = fmaxf(x, xor_lane<4>(x));
+          x = fmaxf(x, xor_lane<8>(x));
+          return fmaxf(x, xor_lane<16>(x));
+        };
+        const float scA = tile_score(0, ntA);
+        const float mtA = max32(scA);
+        const float mA = m_run > mtA ? m_run : mtA;          // m after tile A
+        float mB = mA;                                       // m after tile B
+        float scB = -__builtin_inff();
+        if (ntB > 0) {
+          scB = tile_score(1, ntB);
+          const float mtB = max32(scB);
+          mB = mA > mtB ? mA : mtB;
         }
+        const float sc = tile ? scB : scA;
+        const float m_prev = tile ? mA : m_run, m_new = tile ? mB : mA;
+        const int ntt = tile ? ntB : ntA;
+        const float alpha = exp_s(m_prev - m_new);
+        const float p = t < ntt ? exp_s(sc - m_new) : 0.0f;
+        pb[(tile * MLA_HP + h) * ATT_T + t] = bf16r(p);
+        float ps0 = 0.0f, ps1 = 0.0f;
+#pragma unroll
+        for (int u = 0; u < 32; ++u) {
+          ps0 = ps0 + __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, p), u));
+          ps1 = ps1 + __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, p), 32 + u));
+        }
+        const float ps = h ? ps1 : ps0;
+        if (t == 0) {
+          hs[h * 4 + 2 + tile] = alpha;
+          if (tile) psB[h] = ps;
+        }
+        if (tile == 0) l_run = l_run * alpha + ps;
+        m_run = mB;   // waves 0 and 1 track the same m
       }
       __syncthreads();
       if (done == 0 && t0 == lo) prof_mark(env, 5);
+      if (threadIdx.x < 64) {
+        // wave 0 folds tile B's sum into l and publishes (m, l) for the split's output
+        const int h = (threadIdx.x >> 5) & 1, t = threadIdx.x & 31;
+        if (ntB > 0) l_run = l_run * hs[h * 4 + 3] + psB[h];
+        if (t == 0) {
+          hs[h * 4 + 0] = m_run;
+          hs[h * 4 + 1] = l_run;
+        }
+      }
       // value products, tile A and tile B side by side, each sequential in t:
       // tp[c] = sum_t bf16(p_t) v_t[c]; acc = acc * alpha_A + tp_A, then acc * alpha_B + tp_B
       {
         float tp[4] = {0.0f, 0.0f, 0.0f, 0.0f}, tq[4] = {0.0f, 0.0f, 0.0f, 0.0f};
         const float* pA = pb + ph * ATT_T;
         const float* pB = pb + (MLA_HP + ph) * ATT_T;
-        // 8 rows of each tile loaded at a time, then their fmas in t order (rows past a tile's end
-        // carry p = 0 and are skipped: their staged rows are stale)
-        for (int t8 = 0; t8 < ntA; t8 += 8) {
-          u32x2 kv[8], kv2[8];
-          float pv[8], pv2[8];
+        auto rows8 = [&](int t8, u32x2* kv, u32x2* kv2, float* pv, float* pv2) {
 #pragma unroll
           for (int u = 0; u < 8; ++u) {
             kv[u] = *(const u32x2*)(buf + (t8 + u) * ATT_ROW + pc);
@@ -385,19 +405,53 @@ __device__ __forceinline__ void op_mla_attend(const fx_stage& s, FxEnv& env) {
             pv[u] = pA[t8 + u];
             pv2[u] = pB[t8 + u];
           }
+        };
+        if (ntA == ATT_T && ntB == ATT_T) {
+          // two full tiles: no row tests
 #pragma unroll
-          for (int u = 0; u < 8; ++u) {
-            if (t8 + u < ntA) {
+          for (int t8 = 0; t8 < ATT_T; t8 += 8) {
+            u32x2 kv[8], kv2[8];
+            float pv[8], pv2[8];
+            rows8(t8, kv, kv2, pv, pv2);
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
               tp[0] = __builtin_fmaf(pv[u], bf_lo(kv[u].x), tp[0]);
-              tp[1] = __builtin_fmaf(pv[u], bf_hi(kv[u].x), tp[1]);
-              tp[2] = __builtin_fmaf(pv[u], bf_lo(kv[u].y), tp[2]);
-              tp[3] = __builtin_fmaf(pv[u], bf_hi(kv[u].y), tp[3]);
-            }
-            if (t8 + u < ntB) {
               tq[0] = __builtin_fmaf(pv2[u], bf_lo(kv2[u].x), tq[0]);
+              tp[1] = __builtin_fmaf(pv[u], bf_hi(kv[u].x), tp[1]);
               tq[1] = __builtin_fmaf(pv2[u], bf_hi(kv2[u].x), tq[1]);
+              tp[2] = __builtin_fmaf(pv[u], bf_lo(kv[u].y), tp[2]);
               tq[2] = __builtin_fmaf(pv2[u], bf_lo(kv2[u].y), tq[2]);
+              tp[3] = __builtin_fmaf(pv[u], bf_hi(kv[u].y), tp[3]);
               tq[3] = __builtin_fmaf(pv2[u], bf_hi(kv2[u].y), tq[3]);
+            }
+          }
+        } else {
+          // 8 rows of each tile loaded at a time, then their fmas in t order (rows past a tile's end
+          // carry p = 0 and are skipped: their staged rows are stale)
+          for (int t8 = 0; t8 < ntA; t8 += 8) {
+            u32x2 kv[8], kv2[8];
+            float pv[8], pv2[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+              kv[u] = *(const u32x2*)(buf + (t8 + u) * ATT_ROW + pc);
+              kv2[u] = *(const u32x2*)(buf + (ATT_T + t8 + u) * ATT_ROW + pc);
+              pv[u] = pA[t8 + u];
+              pv2[u] = pB[t8 + u];
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+              if (t8 + u < ntA) {
+                tp[0] = __builtin_fmaf(pv[u], bf_lo(kv[u].x), tp[0]);
+                tp[1] = __builtin_fmaf(pv[u], bf_hi(kv[u].x), tp[1]);
+                tp[2] = __builtin_fmaf(pv[u], bf_lo(kv[u].y), tp[2]);
+                tp[3] = __builtin_fmaf(pv[u], bf_hi(kv[u].y), tp[3]);
+              }
+              if (t8 + u < ntB) {
+                tq[0] = __builtin_fmaf(pv2[u], bf_lo(kv2[u].x), tq[0]);
+                tq[1] = __builtin_fmaf(pv2[u], bf_hi(kv2[u].x), tq[1]);
+                tq[2] = __builtin_fmaf(pv2[u], bf_lo(kv2[u].y), tq[2]);
+                tq[3] = __builtin_fmaf(pv2[u], bf_hi(kv2[u].y), tq[3]);
+              }
             }
           }
         }
