@@ -222,10 +222,22 @@ __device__ __forceinline__ void op_moe_w2(const fx_stage& s, FxEnv& env) {
   auto rowB = [&](int g, int i) { return ids[g / quads] * H + r0 + (g % quads) * 4 + i; };
   Tile<4, 3> t0;
   gemv_prime(t0, W, I, nA, rowA);
+  // the usual split (2 quads per worker: one shared and three routed groups per wave): the routed
+  // tiles of the wave are requested as soon as the routing is known (the third once the shared
+  // tile is consumed), before the routed activations are awaited, so the down weights stream
+  // while the slowest gate|up worker finishes
+  const bool whole = nA == FX_WAVES && nB == 3 * FX_WAVES;
   if (wave_id() == 0) {
     float* lg = red + 256;
     poll_logits_wave(lg, (const void*)s.aux[0], E, tag_in(s, env, 1), env.err);
     route_slots_wave(lg, s, ids, wts, nullptr);
+  }
+  Tile<4, 3> tr0, tr1;
+  if (whole) {
+    __syncthreads();   // ids
+    const int w = wave_id();
+    tile_load(tr0, W, I, w, rowB);
+    tile_load(tr1, W, I, w + FX_WAVES, rowB);
   }
   if (threadIdx.x < (nrow >> 2)) {
     u32x4 v[1];
@@ -249,16 +261,35 @@ __device__ __forceinline__ void op_moe_w2(const fx_stage& s, FxEnv& env) {
       for (int i = 0; i < 4; ++i) o8[sl * W2_ROWS + (g % quads) * 4 + i] = bf16r(acc[i]);
     }
   };
-  gemv_pipe_x(t0, W, I, [&](int g) { return (const float*)(xs + (topk + g / quads) * I); }, nA, rowA,
-              [&](int g, const int* row, const float* acc) { emit(topk, g, acc); });
-  prof_mark(env, 4);
-  // routed slots
-  gemv_prime(t0, W, I, nB, rowB);
-  poll_row(xs, (const void*)s.x, topk * I, tact, env.err);
-  __syncthreads();
-  prof_mark(env, 5);
-  gemv_pipe_x(t0, W, I, [&](int g) { return (const float*)(xs + (g / quads) * I); }, nB, rowB,
-              [&](int g, const int* row, const float* acc) { emit(0, g, acc); });
+  if (whole) {
+    float acc[4];
+    const int g = wave_id();
+    tile_dot(t0, xs + (topk + g / quads) * I, I, acc);
+    emit(topk, g, acc);
+    // the third routed tile reuses the shared tile's registers
+    tile_load(t0, W, I, g + 2 * FX_WAVES, rowB);
+    prof_mark(env, 4);
+    poll_row(xs, (const void*)s.x, topk * I, tact, env.err);
+    __syncthreads();
+    prof_mark(env, 5);
+    tile_dot(tr0, xs + (g / quads) * I, I, acc);
+    emit(0, g, acc);
+    tile_dot(tr1, xs + ((g + FX_WAVES) / quads) * I, I, acc);
+    emit(0, g + FX_WAVES, acc);
+    tile_dot(t0, xs + ((g + 2 * FX_WAVES) / quads) * I, I, acc);
+    emit(0, g + 2 * FX_WAVES, acc);
+  } else {
+    gemv_pipe_x(t0, W, I, [&](int g) { return (const float*)(xs + (topk + g / quads) * I); }, nA, rowA,
+                [&](int g, const int* row, const float* acc) { emit(topk, g, acc); });
+    prof_mark(env, 4);
+    // routed slots
+    gemv_prime(t0, W, I, nB, rowB);
+    poll_row(xs, (const void*)s.x, topk * I, tact, env.err);
+    __syncthreads();
+    prof_mark(env, 5);
+    gemv_pipe_x(t0, W, I, [&](int g) { return (const float*)(xs + (g / quads) * I); }, nB, rowB,
+                [&](int g, const int* row, const float* acc) { emit(0, g, acc); });
+  }
   __syncthreads();
   if (threadIdx.x < nrow) {
     const int r = threadIdx.x;
