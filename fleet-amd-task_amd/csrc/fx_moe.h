@@ -77,9 +77,9 @@ __device__ __forceinline__ void op_moe_router(const fx_stage& s, FxEnv& env) {
   prof_mark(env, 2);
 }
 
-// FX_OP_MOE_W13 over every worker: worker w owns pair groups [q0, q1) (2 pairs each) of every slot's
-// expert; shared slots first, so their weights stream while the router logits are still on their
-// way. With FX_F_ROUTER the stage also computes the router (row e on worker e, W_gate in `res`) and
+// FX_OP_MOE_W13 over every worker: the shared slots' pair groups (2 pairs each) and the routed
+// slots' pair groups are each split evenly over the workers; shared slots first, so their weights
+// stream while the router logits are still on their way. With FX_F_ROUTER the stage also computes the router (row e on worker e, W_gate in `res`) and
 // reads the logits back from its own packets. act8[slot][i] = bf16(silu(bf16(W13[e][i] h)) *
 // bf16(W13[e][I + i] h)).
 __device__ __forceinline__ void op_moe_w13(const fx_stage& s, FxEnv& env) {
@@ -92,20 +92,26 @@ __device__ __forceinline__ void op_moe_w13(const fx_stage& s, FxEnv& env) {
   const bool router = (s.flags & FX_F_ROUTER) != 0;
   const bool writer = env.worker == 0;
   float* lg = red + 256;
-  int q0, q1;
-  range_split(I >> 1, env.nworkers, env.worker, q0, q1);
-  const int nq = q1 - q0;
-  const int nA = nsh * nq, nB = topk * nq;
+  // pair groups (2 pairs = rows p, I + p, p + 1, I + p + 1) of a slot: PG = I / 2. The shared
+  // slots' nsh * PG groups and the routed slots' topk * PG groups are each split evenly over the
+  // workers, so every worker streams the same number of rows (within one group)
+  const int PG = I >> 1;
+  int a0, a1, b0, b1;
+  range_split(nsh * PG, env.nworkers, env.worker, a0, a1);
+  range_split(topk * PG, env.nworkers, env.worker, b0, b1);
+  const int nA = a1 - a0, nB = b1 - b0;
   const uint16_t* W = (const uint16_t*)s.w;
   const size_t ex = (size_t)2 * I;   // rows per expert
   auto rowA = [&](int g, int i) {
-    const int e = E + g / nq;
-    const int p = 2 * (q0 + g % nq) + (i >> 1);
+    const int a = a0 + g;
+    const int e = E + a / PG;
+    const int p = 2 * (a % PG) + (i >> 1);
     return (int)(e * ex + ((i & 1) ? I + p : p));
   };
   auto rowB = [&](int g, int i) {
-    const int e = ids[g / nq];
-    const int p = 2 * (q0 + g % nq) + (i >> 1);
+    const int r = b0 + g;
+    const int e = ids[r / PG];
+    const int p = 2 * (r % PG) + (i >> 1);
     return (int)(e * ex + ((i & 1) ? I + p : p));
   };
   Tile<4, 4> t0;
@@ -128,9 +134,10 @@ __device__ __forceinline__ void op_moe_w13(const fx_stage& s, FxEnv& env) {
   prof_mark(env, 4);
   void* act = (void*)s.out;
   const int half = I >> 1;
-  // act values of the worker's groups: LDS [slot][nq][2], published after the stream
+  // act values of the worker's groups: LDS [shared groups, then routed groups][2], published after
+  // each stream; group a / r of a slot's PG groups is act packet slot * half + (a or r) % PG
   float* actl = (float*)(env.lds + LDS_RES);
-  auto emit = [&](int slot_base, int g, const float* acc) {
+  auto emit = [&](int base, int g, const float* acc) {
     float a[2];
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
@@ -139,16 +146,15 @@ __device__ __forceinline__ void op_moe_w13(const fx_stage& s, FxEnv& env) {
       a[q] = silu_s(gv) * uv;
     }
     if (lane_id() == 0) {
-      const int i = (slot_base + g / nq) * nq + g % nq;
-      actl[2 * i] = a[0];
-      actl[2 * i + 1] = a[1];
+      actl[2 * (base + g)] = a[0];
+      actl[2 * (base + g) + 1] = a[1];
     }
   };
-  gemv_pipe(t0, W, K, xs, nA, rowA, [&](int g, const int* row, const float* acc) { emit(topk, g, acc); });
+  gemv_pipe(t0, W, K, xs, nA, rowA, [&](int g, const int* row, const float* acc) { emit(0, g, acc); });
   __syncthreads();
   if (threadIdx.x < nA) {
-    const int i = topk * nq + threadIdx.x;
-    pk_put(act, (uint32_t)((topk + threadIdx.x / nq) * half + q0 + threadIdx.x % nq), pack2(actl[2 * i], actl[2 * i + 1]),
+    const int a = a0 + threadIdx.x;
+    pk_put(act, (uint32_t)((topk + a / PG) * half + a % PG), pack2(actl[2 * threadIdx.x], actl[2 * threadIdx.x + 1]),
            tag);
   }
   prof_mark(env, 5);
@@ -188,11 +194,13 @@ __device__ __forceinline__ void op_moe_w13(const fx_stage& s, FxEnv& env) {
   __syncthreads();
   prof_mark(env, 6);
   gemv_prime(t0, W, K, nB, rowB);
-  gemv_pipe(t0, W, K, xs, nB, rowB, [&](int g, const int* row, const float* acc) { emit(0, g, acc); });
+  gemv_pipe(t0, W, K, xs, nB, rowB, [&](int g, const int* row, const float* acc) { emit(nA, g, acc); });
   __syncthreads();
-  if (threadIdx.x < nB)
-    pk_put(act, (uint32_t)((threadIdx.x / nq) * half + q0 + threadIdx.x % nq),
-           pack2(actl[2 * threadIdx.x], actl[2 * threadIdx.x + 1]), tag);
+  if (threadIdx.x < nB) {
+    const int r = b0 + threadIdx.x;
+    const int i = nA + threadIdx.x;
+    pk_put(act, (uint32_t)((r / PG) * half + r % PG), pack2(actl[2 * i], actl[2 * i + 1]), tag);
+  }
   prof_mark(env, 2);
 }
 
