@@ -19,6 +19,7 @@ struct FxEnv {
   uint32_t* err;          // the run's error flag
   uint64_t* pst;          // profile stamps of this stage and worker, or null
   char* lds;
+  uint32_t route_tag;     // tag of the router logits whose routing (expert ids, weights) is in LDS, 0: none
 };
 
 // tag that packet input k of stage s carries / that this stage's outputs carry

@@ -192,6 +192,8 @@ __device__ __forceinline__ void op_moe_w13(const fx_stage& s, FxEnv& env) {
     }
   }
   __syncthreads();
+  // the routing stays in LDS for the expert-down stage that follows on this worker
+  env.route_tag = router ? tag : tag_in(s, env, 0);
   prof_mark(env, 6);
   gemv_prime(t0, W, K, nB, rowB);
   gemv_pipe(t0, W, K, xs, nB, rowB, [&](int g, const int* row, const float* acc) { emit(nA, g, acc); });
@@ -235,14 +237,17 @@ __device__ __forceinline__ void op_moe_w2(const fx_stage& s, FxEnv& env) {
   // tile is consumed), before the routed activations are awaited, so the down weights stream
   // while the slowest gate|up worker finishes
   const bool whole = nA == FX_WAVES && nB == 3 * FX_WAVES;
-  if (wave_id() == 0) {
+  // the routing: left in LDS by the gate|up stage of this layer on this worker (persistent kernel),
+  // else from the logits
+  const bool routed_here = env.route_tag == tag_in(s, env, 1);
+  if (!routed_here && wave_id() == 0) {
     float* lg = red + 256;
     poll_logits_wave(lg, (const void*)s.aux[0], E, tag_in(s, env, 1), env.err);
     route_slots_wave(lg, s, ids, wts, nullptr);
   }
   Tile<4, 3> tr0, tr1;
   if (whole) {
-    __syncthreads();   // ids
+    if (!routed_here) __syncthreads();   // ids
     const int w = wave_id();
     tile_load(tr0, W, I, w, rowB);
     tile_load(tr1, W, I, w + FX_WAVES, rowB);

@@ -53,6 +53,7 @@ __device__ __forceinline__ void env_init(FxEnv& env, char* lds, int64_t* tokens,
   env.lds = lds;
   env.pst = nullptr;
   env.token = -1;
+  env.route_tag = 0;
 }
 
 __device__ __forceinline__ void persistent_body(const FxRunArgs& a) {
