@@ -151,15 +151,10 @@ __device__ __forceinline__ void op_moe_w13(const fx_stage& s, FxEnv& env) {
     }
   };
   gemv_pipe(t0, W, K, xs, nA, rowA, [&](int g, const int* row, const float* acc) { emit(0, g, acc); });
-  __syncthreads();
-  if (threadIdx.x < nA) {
-    const int a = a0 + threadIdx.x;
-    pk_put(act, (uint32_t)((topk + a / PG) * half + a % PG), pack2(actl[2 * threadIdx.x], actl[2 * threadIdx.x + 1]),
-           tag);
-  }
   prof_mark(env, 5);
-  // routed slots: the top-k of the logits
-  if (wave_id() == 0) {
+  // routed slots: the top-k of the logits, on the last wave (groups g = wave, wave + 4, ..: it has
+  // the fewest shared groups, so it polls the logits while the others finish theirs)
+  if (wave_id() == FX_WAVES - 1) {
     poll_logits_wave(lg, (const void*)s.aux[0], E, router ? tag : tag_in(s, env, 0), env.err);
     float* probs = red + 512;
     route_slots_wave(lg, s, ids, wts, probs);
@@ -192,6 +187,11 @@ __device__ __forceinline__ void op_moe_w13(const fx_stage& s, FxEnv& env) {
     }
   }
   __syncthreads();
+  if (threadIdx.x < nA) {
+    const int a = a0 + threadIdx.x;
+    pk_put(act, (uint32_t)((topk + a / PG) * half + a % PG), pack2(actl[2 * threadIdx.x], actl[2 * threadIdx.x + 1]),
+           tag);
+  }
   // the routing stays in LDS for the expert-down stage that follows on this worker
   env.route_tag = router ? tag : tag_in(s, env, 0);
   prof_mark(env, 6);
