@@ -7,22 +7,134 @@ reference's harness/compare.py (compare_ids :161-178, compare_route_log :181-236
 
 Reference-side files: ref_output_ids.json, ref_route_log.json ([step][moe layer] {"idx": [...],
 optional "w_all": [64 router weights]}). Fleet-side files (written by run_fleet.py):
-fleet_output_ids.json, fleet_route_log.json, fleet_run_meta.json.
+fleet_output_ids.json, fleet_route_log.json, fleet_run_meta.json, fleet_boundaries.safetensors.
+With ref_boundaries_step0.safetensors (and ref_boundaries_step{iters-1}.safetensors for a run of
+several iterations) the boundaries are judged too; calibration.json ({"floor": {class: value}},
+default <ref>/calibration.json) replaces each class threshold by 4 x its floor.
 
-The exact checks keep the reference's rules: the ids are compared as a prefix (PASS when all
-match, PARTIAL when a shorter run matched every id it produced, FAIL at the first divergence); the
-route log per (step, MoE layer) as a sorted set of the reference's top-k (the Fleet log may append
-the forced shared experts). Without "w_all" any route difference fails; with it a single swap whose
-two router weights lie within tol_rel of the larger is a tie, later mismatches of the same run are
-cascades, and only the rest (disagreements) fail. This build's boundary tensors are not dumped
-yet, so the per-boundary metrics of the reference's compare are not part of this verdict.
+The checks keep the reference's rules (compare.py:36-236):
+  * boundaries: rel_err = |fleet - ref|_2 / |ref|_2 (FP64) against the class threshold; B9 (top-k
+    ids) as a set and B16 (token) exactly; B10 (top-k weights) aligned by expert id through B9; a key
+    of a layer the reference did not capture is NOT_CAPTURED, a later-iteration key without the
+    reference's file for that step NOT_COMPARABLE (neither counts), a key the reference lacks
+    MISSING_REF (fails the run);
+  * ids: a prefix (PASS when all match, PARTIAL when a shorter run matched every id it produced,
+    FAIL at the first divergence);
+  * route log per (step, MoE layer): a sorted set of the reference's top-k (the Fleet log may append
+    the forced shared experts). Without "w_all" any route difference fails; with it a single swap
+    whose two router weights lie within tol_rel of the larger is a tie, later mismatches of the same
+    run are cascades, and only the rest (disagreements) fail.
+Overall PASS: no FAIL, no MISSING_REF, and at least one check passed.
 """
 import argparse
 import json
+import math
+import re
 import sys
 from pathlib import Path
 
+import numpy as np
+
+sys.path.insert(0, str(Path(__file__).resolve().parent))
+import boundaries as BD  # noqa: E402
+
 ROUTE_TOL = 0.015   # the reference's fallback: 4 x its calibrated router floor (3.59e-3)
+
+
+def metrics(a, b):
+    """a = Fleet, b = reference, both flattened to FP64: max |a - b|, |a - b|_2 / |b|_2, cos(a, b)."""
+    a = np.asarray(a, np.float64).reshape(-1)
+    b = np.asarray(b, np.float64).reshape(-1)
+    if a.size != b.size:
+        return {"shape_mismatch": [a.size, b.size]}
+    d = a - b
+    na, nb = float(np.linalg.norm(a)), float(np.linalg.norm(b))
+    mx = float(np.abs(d).max()) if d.size else 0.0
+    rel = float(np.linalg.norm(d)) / nb if nb > 0 else (0.0 if mx == 0 else math.inf)
+    cos = float(np.dot(a, b)) / (na * nb) if na > 0 and nb > 0 else (1.0 if mx == 0 else 0.0)
+    return {"max_abs_err": mx, "rel_err": rel, "cos_sim": cos, "n": int(a.size)}
+
+
+def thresholds(calibration):
+    """(class -> rel_err threshold, where the thresholds came from)."""
+    th = dict(BD.CLASS_THRESHOLD)
+    if not calibration or "floor" not in calibration:
+        return th, "starting values (not calibrated)"
+    for cls, floor in calibration["floor"].items():
+        if cls in th and cls != "exact":
+            th[cls] = BD.THRESHOLD_MULTIPLIER * float(floor)
+    return th, f"{BD.THRESHOLD_MULTIPLIER:g} x calibrated floor"
+
+
+def _ids_by_weight(key, side):
+    k9 = key.replace(".B10.topk_w", ".B9.topk_idx")
+    if k9 not in side:
+        return None
+    return dict(zip(np.asarray(side[k9]).reshape(-1).astype(np.int64).tolist(),
+                    np.asarray(side[key], np.float64).reshape(-1).tolist()))
+
+
+def _sort_key(key):
+    m = re.match(r"^L(\d+)\.B(\d+)\.", key)
+    if m:
+        return (int(m.group(1)), int(m.group(2)), key)
+    m = re.match(r"^L(\d+)\.", key)
+    return (int(m.group(1)), 99, key) if m else (10 ** 6, 0, key)
+
+
+def compare_boundaries(ref, fleet, th, floor=None, iters=1, ref_later=None):
+    """One row per boundary key of the Fleet file (auxiliary tensors skipped)."""
+    rows = []
+    ref_layers = sorted({int(k.split(".")[0][1:]) for k in ref if re.match(r"^L\d+\.", k)})
+    for key in sorted(fleet, key=_sort_key):
+        cls = BD.boundary_class(key)
+        if cls is None:
+            continue
+        row = {"key": key, "boundary": BD.boundary_id(key), "class": cls}
+        rows.append(row)
+        m = re.match(r"^L(\d+)\.", key)
+        if m and int(m.group(1)) not in ref_layers:
+            row.update(result="NOT_CAPTURED", detail=f"the reference captures layers {ref_layers}")
+            continue
+        it = BD.boundary_iteration(key, iters)
+        side = ref
+        if it > 0:
+            row["iteration"] = it
+            if ref_later is None:
+                row.update(result="NOT_COMPARABLE",
+                           detail=f"dumped from iteration {it}; the reference has no ref_boundaries_step{it}")
+                continue
+            side = ref_later
+        if key not in side:
+            row["result"] = "MISSING_REF"
+            continue
+        a, b = fleet[key], side[key]
+        if row["boundary"] == "B9":
+            fa = sorted(np.asarray(a).reshape(-1).astype(np.int64).tolist())
+            fb = sorted(np.asarray(b).reshape(-1).astype(np.int64).tolist())
+            row.update(result="PASS" if fa == fb else "FAIL", detail=f"fleet {fa} ref {fb}")
+            continue
+        if cls == "exact":
+            va, vb = int(np.asarray(a).reshape(-1)[0]), int(np.asarray(b).reshape(-1)[0])
+            row.update(result="PASS" if va == vb else "FAIL", detail=f"fleet {va} ref {vb}")
+            continue
+        if row["boundary"] == "B10":
+            # the reference's top-k order is unspecified: weights matched by expert id
+            fa, rb = _ids_by_weight(key, fleet), _ids_by_weight(key, side)
+            if fa is not None and rb is not None:
+                if set(fa) != set(rb):
+                    row.update(result="FAIL", detail=f"expert sets differ: fleet {sorted(fa)} ref {sorted(rb)}")
+                    continue
+                a, b = [fa[e] for e in sorted(rb)], [rb[e] for e in sorted(rb)]
+        mt = metrics(a, b)
+        if "shape_mismatch" in mt:
+            row.update(result="FAIL", detail=f"shape mismatch {mt['shape_mismatch']}")
+            continue
+        row.update(mt)
+        row["threshold"] = th[cls]
+        row["floor"] = floor.get(cls) if floor else None
+        row["result"] = "PASS" if mt["rel_err"] <= th[cls] else "FAIL"
+    return rows
 
 
 def compare_ids(ref_ids, fleet_ids):
@@ -40,6 +152,7 @@ def compare_ids(ref_ids, fleet_ids):
 
 
 def compare_route_log(ref_log, fleet_log, tol_rel=ROUTE_TOL):
+    """tol_rel: ROUTE_TOL, or THRESHOLD_MULTIPLIER x the calibrated router floor."""
     has_w = bool(ref_log) and all("w_all" in e for step in ref_log for e in step)
     mismatches, ties, cascades, disagreements = [], [], [], []
     steps = min(len(ref_log), len(fleet_log))
@@ -80,10 +193,30 @@ def compare_route_log(ref_log, fleet_log, tol_rel=ROUTE_TOL):
             "result": result}
 
 
-def run(ref_dir: Path, fleet_dir: Path, report: Path):
+def _fmt(x, nd=3):
+    if x is None:
+        return "-"
+    if isinstance(x, float):
+        return f"{x:.{nd}e}" if (x != 0 and abs(x) < 1e-2) else f"{x:.{nd}f}"
+    return str(x)
+
+
+def run(ref_dir: Path, fleet_dir: Path, report: Path, calibration_path: Path = None):
     meta_p = fleet_dir / "fleet_run_meta.json"
     meta = json.loads(meta_p.read_text()) if meta_p.exists() else {}
-    result = {"ref": str(ref_dir), "fleet": str(fleet_dir)}
+    iters = int(meta.get("iters", 1) or 1)
+    cal_p = calibration_path if calibration_path is not None else ref_dir / "calibration.json"
+    calibration = json.loads(cal_p.read_text()) if cal_p.exists() else None
+    th, source = thresholds(calibration)
+    floor = calibration.get("floor") if calibration else None
+    result = {"ref": str(ref_dir), "fleet": str(fleet_dir), "iters": iters, "threshold_source": source,
+              "thresholds": th}
+    f_b, r_b = fleet_dir / "fleet_boundaries.safetensors", ref_dir / "ref_boundaries_step0.safetensors"
+    if f_b.exists() and r_b.exists():
+        later = ref_dir / f"ref_boundaries_step{iters - 1}.safetensors"
+        ref_later = BD.read(later) if iters > 1 and later.exists() else None
+        result["later_reference"] = later.name if ref_later is not None else None
+        result["boundaries"] = compare_boundaries(BD.read(r_b), BD.read(f_b), th, floor, iters, ref_later)
     f_ids = fleet_dir / "fleet_output_ids.json"
     if f_ids.exists() and meta.get("head", True) and not meta.get("stop_after"):
         result["output_ids"] = compare_ids(json.loads((ref_dir / "ref_output_ids.json").read_text()),
@@ -92,13 +225,36 @@ def run(ref_dir: Path, fleet_dir: Path, report: Path):
         result["output_ids"] = {"result": "SKIP", "note": "truncated graph: no head, ids are placeholders"}
     f_route = fleet_dir / "fleet_route_log.json"
     if f_route.exists():
+        tol = BD.THRESHOLD_MULTIPLIER * float(floor["router"]) if floor and floor.get("router") else ROUTE_TOL
         result["route_log"] = compare_route_log(json.loads((ref_dir / "ref_route_log.json").read_text()),
-                                                json.loads(f_route.read_text()))
-    verdicts = [result[k]["result"] for k in ("output_ids", "route_log") if k in result]
-    checked = [v for v in verdicts if v != "SKIP"]
-    result["overall"] = "PASS" if checked and all(v in ("PASS", "PARTIAL") for v in checked) else "FAIL"
+                                                json.loads(f_route.read_text()), tol)
+    verdicts = [r["result"] for r in result.get("boundaries", [])]
+    verdicts += [result[k]["result"] for k in ("output_ids", "route_log") if k in result and result[k]["result"] != "SKIP"]
+    result["n_pass"] = verdicts.count("PASS") + verdicts.count("PARTIAL")
+    result["n_fail"] = verdicts.count("FAIL")
+    result["n_missing"] = verdicts.count("MISSING_REF")
+    result["n_not_comparable"] = verdicts.count("NOT_COMPARABLE")
+    result["n_not_captured"] = verdicts.count("NOT_CAPTURED")
+    result["overall"] = "PASS" if result["n_fail"] == 0 and result["n_missing"] == 0 and result["n_pass"] > 0 else "FAIL"
     report.parent.mkdir(parents=True, exist_ok=True)
-    lines = ["# correctness report", "", f"reference: `{ref_dir}`  fleet: `{fleet_dir}`", ""]
+    lines = ["# correctness report", "", f"reference: `{ref_dir}`  fleet: `{fleet_dir}`",
+             f"thresholds: {source}", ""]
+    if result.get("boundaries"):
+        if iters > 1:
+            lines += [f"The run made {iters} iterations: boundaries other than the cache rows and the first token "
+                      f"come from iteration {iters - 1}" + (f", compared against `{result['later_reference']}`."
+                                                            if result.get("later_reference") else
+                                                            " and are not comparable with the reference's step 0."), ""]
+        lines += ["| key | boundary | class | max_abs_err | rel_err | cos_sim | threshold | result |",
+                  "|---|---|---|---|---|---|---|---|"]
+        for r in result["boundaries"]:
+            if "rel_err" in r:
+                lines.append(f"| `{r['key']}` | {r['boundary']} | {r['class']} | {_fmt(r['max_abs_err'])} | "
+                             f"{_fmt(r['rel_err'])} | {_fmt(r['cos_sim'], 5)} | {_fmt(r['threshold'])} | **{r['result']}** |")
+            else:
+                lines.append(f"| `{r['key']}` | {r['boundary']} | {r['class']} | - | - | - | - | "
+                             f"**{r['result']}** {r.get('detail', '')} |")
+        lines.append("")
     for k in ("output_ids", "route_log"):
         if k in result:
             r = result[k]
@@ -109,7 +265,9 @@ def run(ref_dir: Path, fleet_dir: Path, report: Path):
                 extra = (f" ({r['steps_compared']} steps, rule {r['rule']}: {len(r['mismatches'])} mismatches, "
                          f"{len(r['ties'])} ties, {len(r['cascades'])} cascades, {len(r['disagreements'])} disagreements)")
             lines.append(f"- {k}: **{r['result']}**{extra}")
-    lines += ["", f"overall: **{result['overall']}**", ""]
+    lines += ["", f"overall: **{result['overall']}** ({result['n_pass']} pass, {result['n_fail']} fail, "
+                  f"{result['n_missing']} missing, {result['n_not_comparable']} not comparable, "
+                  f"{result['n_not_captured']} not captured)", ""]
     report.write_text("\n".join(lines))
     report.with_suffix(".json").write_text(json.dumps(result, indent=2) + "\n")
     return result
@@ -120,10 +278,14 @@ def main(argv=None):
     ap.add_argument("--ref", required=True)
     ap.add_argument("--fleet", required=True)
     ap.add_argument("--report", default=None, help="default: <fleet>/correctness_report.md")
+    ap.add_argument("--calibration", default=None, help="calibration.json (default: <ref>/calibration.json)")
     args = ap.parse_args(argv)
     ref_dir, fleet_dir = Path(args.ref), Path(args.fleet)
     report = Path(args.report) if args.report else fleet_dir / "correctness_report.md"
-    result = run(ref_dir, fleet_dir, report)
+    result = run(ref_dir, fleet_dir, report, Path(args.calibration) if args.calibration else None)
+    for r in result.get("boundaries", []):
+        extra = f" rel_err {_fmt(r.get('rel_err'))} thr {_fmt(r.get('threshold'))}" if "rel_err" in r else f" {r.get('detail', '')}"
+        print(f"{r['result']:14s} {r['key']:28s}{extra}")
     for k in ("output_ids", "route_log"):
         if k in result:
             print(f"{result[k]['result']:12s} {k}")

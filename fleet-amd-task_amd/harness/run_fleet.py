@@ -18,6 +18,9 @@ Files written to --out (the reference's names and formats):
   fleet_run_meta.json    the run's arguments, sizes, device buffer addresses, outputs, "completed"
   fleet_output_ids.json  the greedy ids at positions n_prompt .. n_prompt + iters - 1
   fleet_route_log.json   [step][moe layer] {"idx": [8 expert ids], "w": []}
+  fleet_boundaries.safetensors  the boundary tensors under the reference's keys (harness/boundaries.py):
+                         decode step 0's when --iters 1, else the last iteration's (cache rows and
+                         the first token are always step 0's)
   event_timing.json      with --event-timing: per-stage timing of the last iteration (fx_set_profile)
   wall.json              wall-clock seconds of the fill, build and run
 Exit status 0 on success; a failed launch raises FxError with the library's message (nonzero exit).
@@ -36,6 +39,9 @@ from fleet import build_graph as B  # noqa: E402
 from fleet import graph_plan as G  # noqa: E402
 from fleet import pack_weights as P  # noqa: E402
 from fleet import runtime as R  # noqa: E402
+
+sys.path.insert(0, str(Path(__file__).resolve().parent))
+import boundaries as BD  # noqa: E402
 
 N_PROMPT = 1024
 SEED = 20261201
@@ -135,6 +141,9 @@ def run(args, rt=None):
         if n_moe and "route_log" in runner.host:
             rl = runner.host["route_log"].download()
             (out / "fleet_route_log.json").write_text(json.dumps(route_log_json(rl, args.iters, n_moe)) + "\n")
+        bnd, notes = BD.dump(pj["calls"], runner.host, n_prompt, d.TOPK, d.Q_OUT, args.iters)
+        BD.write(out / "fleet_boundaries.safetensors", bnd, {"iters": args.iters, "n_prompt": n_prompt})
+        meta_out.update({"boundaries": sorted(bnd), "boundary_notes": notes})
         wall = {"run_wall_s": t_run, "iters": args.iters, "positions": total, "pack_s": t_pack, "build_s": t_build}
         (out / "wall.json").write_text(json.dumps(wall) + "\n")
         meta_out.update({"output_ids": ids, "timings_s": wall, "completed": True})

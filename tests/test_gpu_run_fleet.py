@@ -1,10 +1,12 @@
 """run_fleet.py end to end on the GPU against a reference directory written from the oracle, then
 judged by compare.py: the reference's run_fleet -> compare flow (harness/run_fleet.py:449-616,
-harness/compare.py:318-378) on a 2-layer model."""
+harness/compare.py:318-378) on a 2-layer model, ids, route log and boundary tensors (decode step 0
+and the last iteration, as the reference's F2 rule reads them)."""
 import json
 import sys
 from pathlib import Path
 
+import numpy as np
 import pytest
 
 from oracle import model as M
@@ -13,10 +15,32 @@ from fleet import pack_weights as P
 from fxtest import SEED, GpuWeights
 
 sys.path.insert(0, str(Path(__file__).resolve().parent.parent / "fleet-amd-task_amd" / "harness"))
+import boundaries as BD  # noqa: E402
 import compare as C  # noqa: E402
 import run_fleet as RF  # noqa: E402
 
 pytestmark = pytest.mark.gpu
+
+
+def ref_boundaries(rec, topk):
+    """The reference-side boundary file of one decode step from the oracle's record (the keys of
+    the reference's run_reference capture: B10 the top-k weights only, B11 per expert id, B12 the
+    shared experts' sum in FP32)."""
+    out = {}
+    for k, v in rec.items():
+        if BD.boundary_class(k) is not None:
+            out[k] = np.asarray(v)
+    for k in [k for k in rec if k.endswith(".out8")]:
+        l = k.split(".")[0]
+        ids = rec[f"{l}.mask"][:topk]
+        out8 = rec[k]
+        for s in range(topk):
+            out[f"{l}.B11.expert_{int(ids[s])}"] = out8[s]
+        f = lambda u: (np.asarray(u, np.uint16).astype(np.uint32) << 16).view(np.float32)  # noqa: E731
+        out[f"{l}.B12.shared"] = f(out8[topk]) + f(out8[topk + 1])
+        out[f"{l}.B10.topk_w"] = np.asarray(rec[f"{l}.B10.topk_w"], np.float32)[:topk]
+    out["head.B16.token"] = np.asarray(rec["head.B16.token"], np.int64).reshape(1)
+    return out
 
 
 def test_run_fleet_then_compare(rt, tmp_path):
@@ -37,14 +61,37 @@ def test_run_fleet_then_compare(rt, tmp_path):
                 split=plan.split, n_splits=plan.n_splits)
     cos, sin = M.rope_tables(s_max)
     W = GpuWeights(P.fill_seeded(rt, d, SEED, layers=layers, head=True))
-    ids, routes = M.generate(cfg, W, M.Cache(cfg, s_max, layers), cos, sin,
-                             P.prompt_ids(SEED, ctx, d.V), iters, layers=layers)
+    prompt = P.prompt_ids(SEED, ctx, d.V)
+    cache = M.Cache(cfg, s_max, layers)
+    for pos in range(ctx - 1):
+        M.decode_step(cfg, W, cache, cos, sin, prompt[pos], pos, layers, head=False)
+    ids, routes, recs = [], [], []
+    tok = int(prompt[-1])
+    for i in range(iters):
+        rec = {}
+        tok, r, _ = M.decode_step(cfg, W, cache, cos, sin, tok, ctx - 1 + i, layers, head=True, rec=rec)
+        ids.append(tok)
+        routes.append(r)
+        recs.append(rec)
     ref = tmp_path / "ref"
     ref.mkdir()
     (ref / "ref_output_ids.json").write_text(json.dumps(ids))
     (ref / "ref_route_log.json").write_text(json.dumps([[{"idx": r[:d.TOPK]} for r in step] for step in routes]))
+    BD.write(ref / "ref_boundaries_step0.safetensors", ref_boundaries(recs[0], d.TOPK))
+    BD.write(ref / f"ref_boundaries_step{iters - 1}.safetensors", ref_boundaries(recs[-1], d.TOPK))
     res = C.run(ref, fleet, fleet / "correctness_report.md")
     print(f"[run_fleet] fleet ids {meta['output_ids']} oracle ids {ids}: {res['overall']}", flush=True)
     assert res["output_ids"]["result"] == "PASS", res["output_ids"]
     assert res["route_log"]["result"] == "PASS", res["route_log"]["mismatches"][:3]
-    assert res["overall"] == "PASS"
+    rows = res["boundaries"]
+    keys = {r["key"] for r in rows}
+    for k in ("L1.B2.q", "L0.B3.c_kv", "L1.B3.k_pe", "L1.B4.q_pe", "L1.B6.attn", "L1.B7.x_res_attn",
+              "L1.B8.router_logits", "L1.B9.topk_idx", "L1.B10.topk_w", "L1.B12.shared", "L1.B13.layer_out",
+              "head.B15.logits", "head.B16.token"):
+        assert k in keys, k
+    assert sum(k.startswith("L1.B11.expert_") for k in keys) == d.TOPK
+    bad = [(r["key"], r["result"], r.get("rel_err"), r.get("detail")) for r in rows if r["result"] != "PASS"]
+    assert not bad, bad
+    # this build is bit-exact with the oracle at every boundary
+    assert all(r.get("rel_err", 0.0) == 0.0 for r in rows), [(r["key"], r["rel_err"]) for r in rows if r.get("rel_err")]
+    assert res["overall"] == "PASS" and res["n_not_comparable"] == 0
