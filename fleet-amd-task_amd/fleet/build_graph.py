@@ -286,11 +286,13 @@ def make_meta(rt, s_max, prompt):
     return {"tokens": tokens}
 
 
-def make_capture(rt, plan, cache=None):
+def make_capture(rt, plan, cache=None, tables=None):
     """cos/sin tables and the per-layer latent caches (zeroed, or uploaded from host arrays
-    cache['c_kv'][l], cache['k_pe'][l] for rows [0, len))."""
+    cache['c_kv'][l], cache['k_pe'][l] for rows [0, len)). tables: (cos, sin) bf16 bits [s_max, D_R]
+    of the model (checkpoint.ModelConfig.tables), default plain RoPE with theta 10000."""
     d = plan.dims
-    cos, sin = rope_tables(plan.s_max, d.D_R)
+    cos, sin = tables if tables is not None else rope_tables(plan.s_max, d.D_R)
+    assert cos.shape == (plan.s_max, d.D_R) and sin.shape == cos.shape, (cos.shape, plan.s_max)
     cap = {"cos": rt.alloc(cos.shape, "bf16").upload(cos), "sin": rt.alloc(sin.shape, "bf16").upload(sin)}
     for l in range(plan.layers):
         cap[f"c_kv_{l}"] = rt.alloc((plan.s_max, d.D_C), "bf16").zero()

@@ -146,7 +146,8 @@ def _contig(dst_offset, n, name, src_offset=0):
 class PackedTensor:
     key: str
     shape: tuple
-    init: object            # "ones" or a list of Segment
+    init: object            # "ones" (a norm weight: 1.0 in the seeded model) or a list of Segment
+    source: str = ""        # the HF tensor a "ones" key is loaded from (checkpoint.py)
 
     @property
     def numel(self):
@@ -164,12 +165,12 @@ def seeded_layout(d: Dims = REAL_DIMS, layers: int = None, head: bool = True):
     out = {"W_embed": PackedTensor("W_embed", (d.V, H), [_contig(0, d.V * H, "model.embed_tokens.weight")])}
     if head:
         out["W_lm"] = PackedTensor("W_lm", (d.V, H), [_contig(0, d.V * H, "lm_head.weight")])
-        out["w_final_norm"] = PackedTensor("w_final_norm", (H,), "ones")
+        out["w_final_norm"] = PackedTensor("w_final_norm", (H,), "ones", "model.norm.weight")
     for l in range(L):
         p = f"model.layers.{l}."
-        out[f"w_norm1_{l}"] = PackedTensor(f"w_norm1_{l}", (H,), "ones")
-        out[f"w_norm2_{l}"] = PackedTensor(f"w_norm2_{l}", (H,), "ones")
-        out[f"w_kv_norm_{l}"] = PackedTensor(f"w_kv_norm_{l}", (d.D_C,), "ones")
+        out[f"w_norm1_{l}"] = PackedTensor(f"w_norm1_{l}", (H,), "ones", p + "input_layernorm.weight")
+        out[f"w_norm2_{l}"] = PackedTensor(f"w_norm2_{l}", (H,), "ones", p + "post_attention_layernorm.weight")
+        out[f"w_kv_norm_{l}"] = PackedTensor(f"w_kv_norm_{l}", (d.D_C,), "ones", p + "self_attn.kv_a_layernorm.weight")
         out[f"W_qkva_{l}"] = PackedTensor(f"W_qkva_{l}", (d.Q_OUT + d.KVA_OUT, H), [
             _contig(0, d.Q_OUT * H, p + "self_attn.q_proj.weight"),
             _contig(d.Q_OUT * H, d.KVA_OUT * H, p + "self_attn.kv_a_proj_with_mqa.weight")])

@@ -6,8 +6,10 @@
                                                    [--seed S] [--stop-after L1.o_proj] [--out DIR] [--event-timing]
 
 What differs from the reference, and why:
-  * weights are the seeded bf16 model (fleet/pack_weights.fill_seeded) instead of --model-dir: this
-    build has no checkpoint loader yet, so --model-dir is refused with that message;
+  * without --model-dir the weights are the seeded bf16 model (fleet/pack_weights.fill_seeded,
+    plain RoPE, scale 192^-0.5); with it, the checkpoint's safetensors shards are loaded into the
+    same packed keys (fleet/checkpoint.py) and the config's YaRN tables, softmax scale and norm eps
+    are used;
   * the prompt's cache rows 0 .. n_prompt - 2 are produced by this kernel itself (teacher-forced
     iterations, head skipped) instead of being captured from the HF prefill (--ref's
     ref_cache.safetensors), so the whole run is one fx_run over positions 0 .. n_prompt - 2 + iters;
@@ -38,6 +40,7 @@ sys.path.insert(0, str(PKG))
 from fleet import build_graph as B  # noqa: E402
 from fleet import graph_plan as G  # noqa: E402
 from fleet import pack_weights as P  # noqa: E402
+from fleet import checkpoint as CK  # noqa: E402
 from fleet import runtime as R  # noqa: E402
 
 sys.path.insert(0, str(Path(__file__).resolve().parent))
@@ -62,7 +65,8 @@ def build_parser():
     ap.add_argument("--event-timing", action="store_true", help="per-stage stamps of the last iteration")
     ap.add_argument("--final", action="store_true", help="accepted for the reference's command line; this build "
                                                          "has one configuration")
-    ap.add_argument("--model-dir", default=None, help="not supported: the build fills seeded weights")
+    ap.add_argument("--model-dir", default=None, help="HF snapshot directory (config.json + safetensors shards); "
+                                                      "default: the seeded model")
     return ap
 
 
@@ -81,9 +85,14 @@ def run(args, rt=None):
     """Run the decode described by `args` (build_parser's namespace) and write the run directory.
     Returns the fleet_run_meta dict. `rt`: an existing Runtime (else one is created)."""
     d = P.REAL_DIMS
+    mcfg = None
     if args.model_dir:
-        raise SystemExit("run_fleet: --model-dir is not supported: this build has no checkpoint loader into the "
-                         "packed keys yet; it fills the seeded model (--seed)")
+        if not (Path(args.model_dir) / "config.json").exists():
+            raise SystemExit(f"run_fleet: {args.model_dir} has no config.json (an HF snapshot directory is expected)")
+        mcfg = CK.read_config(args.model_dir)
+        if mcfg.dims != d:
+            raise SystemExit(f"run_fleet: the kernels are built for DeepSeek-V2-Lite's shapes {d}; {args.model_dir} "
+                             f"has {mcfg.dims}")
     layers = args.layers if args.layers is not None else d.L
     if not 1 <= layers <= d.L:
         raise SystemExit(f"run_fleet: --layers must be in [1, {d.L}]")
@@ -104,23 +113,31 @@ def run(args, rt=None):
         rt = R.Runtime(0)
     try:
         t0 = time.time()
-        packed = P.fill_seeded(rt, d, args.seed, layers=layers, head=args.head)
+        if mcfg is not None:
+            packed = CK.load_packed(rt, args.model_dir, d, layers=layers, head=args.head)
+        else:
+            packed = P.fill_seeded(rt, d, args.seed, layers=layers, head=args.head)
         t_pack = time.time() - t0
         t1 = time.time()
         plan_kw = {}
+        if mcfg is not None:
+            plan_kw.update(softmax_scale=mcfg.scale, eps=mcfg.eps)
         if args.split:
             plan_kw["split"] = args.split
         if args.n_splits:
             plan_kw["n_splits"] = args.n_splits
         meta = B.make_meta(rt, s_max, prompt)
-        cap = B.make_capture(rt, G.build_plan(d, s_max, layers, args.head, **plan_kw))
+        cap = B.make_capture(rt, G.build_plan(d, s_max, layers, args.head, **plan_kw),
+                             tables=mcfg.tables(s_max) if mcfg is not None else None)
         runner = B.build(rt, packed, cap, meta, d, s_max, layers, args.head, stop_after=args.stop_after, **plan_kw)
         pj = B.plan_json(runner.plan)
         (out / "plan.json").write_text(json.dumps(pj) + "\n")
         t_build = time.time() - t1
         meta_out = {
             "layers": layers, "head": args.head, "iters": args.iters, "stop_after": args.stop_after,
-            "s_max": s_max, "n_prompt": n_prompt, "seed": args.seed, "split": runner.plan.split,
+            "s_max": s_max, "n_prompt": n_prompt, "seed": None if mcfg else args.seed,
+            "model_dir": args.model_dir, "softmax_scale": runner.plan.scale, "eps": runner.plan.eps,
+            "split": runner.plan.split,
             "n_splits": runner.plan.n_splits, "ops": len(pj["calls"]), "stages": len(runner.stages),
             "device": rt.info(), "addresses": {k: int(v.ptr) for k, v in runner.host.items()}, "completed": False,
         }

@@ -1,0 +1,133 @@
+"""The checkpoint path on the GPU (fleet/checkpoint.py, run_fleet.py --model-dir).
+
+A real-shaped DeepSeek-V2-Lite checkpoint of 2 layers + head is written as safetensors shards with
+an index: every HF tensor is generated whole from its own name's seeded stream on the device (the
+seeded model's definition: each HF tensor is one stream, pack_weights.py), the norm weights are a
+non-trivial pattern, and config.json carries the model's YaRN rope_scaling. Then:
+  * load_packed gives exactly fill_seeded's packed buffers for every weight key (the layout cut
+    the same streams) and the pattern for every norm key;
+  * run_fleet --model-dir decodes with the config's YaRN tables and softmax scale, and compare.py
+    finds the ids, the route log and every boundary equal to the oracle's on the same weights,
+    tables and scale.
+"""
+import json
+import sys
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from oracle import model as M
+from fleet import checkpoint as CK
+from fleet import graph_plan as G
+from fleet import pack_weights as P
+from fxtest import SEED, GpuWeights, ref_boundaries
+
+sys.path.insert(0, str(Path(__file__).resolve().parent.parent / "fleet-amd-task_amd" / "harness"))
+import boundaries as BD  # noqa: E402
+import compare as C  # noqa: E402
+import run_fleet as RF  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+
+CONFIG = {
+    "hidden_size": 2048, "num_attention_heads": 16, "qk_nope_head_dim": 128, "qk_rope_head_dim": 64,
+    "v_head_dim": 128, "kv_lora_rank": 512, "vocab_size": 102400, "num_hidden_layers": 27,
+    "intermediate_size": 10944, "moe_intermediate_size": 1408, "n_routed_experts": 64,
+    "num_experts_per_tok": 6, "n_shared_experts": 2, "rms_norm_eps": 1e-6, "rope_theta": 10000,
+    "rope_scaling": {"type": "yarn", "factor": 40, "original_max_position_embeddings": 4096, "beta_fast": 32,
+                     "beta_slow": 1, "mscale": 0.707, "mscale_all_dim": 0.707},
+}
+
+
+def norm_pattern(n, k):
+    i = np.arange(n, dtype=np.float32)
+    return P.f32_to_bf16(1.0 + 0.05 * np.sin(0.37 * i + k).astype(np.float32))
+
+
+def write_checkpoint(rt, d, layers, out):
+    """Shards per layer (+ one for the embedding and head) and the index; returns the norm values."""
+    shards = {}
+    for name, shape in CK.hf_shapes(d, layers, True).items():
+        shard = (f"model-layer{int(name.split('.')[2]):02d}.safetensors" if name.startswith("model.layers.")
+                 else "model-embed-head.safetensors")
+        shards.setdefault(shard, []).append((name, shape))
+    weight_map, norms = {}, {}
+    for shard, items in shards.items():
+        tensors = {}
+        for name, shape in items:
+            n = int(np.prod(shape))
+            if len(shape) == 1:
+                tensors[name] = norms[name] = norm_pattern(n, len(norms))
+            else:
+                buf = rt.alloc((n,), "bf16")
+                rt.gen_normal_bf16(buf, n, SEED, P.fnv1a32(name), P.WEIGHT_SCALE)
+                tensors[name] = buf.download().reshape(shape)
+                buf.free()
+            weight_map[name] = shard
+        BD.write(out / shard, tensors)
+        del tensors
+    (out / "model.safetensors.index.json").write_text(json.dumps({"metadata": {}, "weight_map": weight_map}))
+    (out / "config.json").write_text(json.dumps(CONFIG))
+    return norms
+
+
+def test_checkpoint_load_and_decode(rt, tmp_path):
+    d, layers, ctx, iters = P.REAL_DIMS, 2, 40, 3
+    model = tmp_path / "model"
+    model.mkdir()
+    print(f"[checkpoint] writing a {layers}-layer checkpoint", flush=True)
+    norms = write_checkpoint(rt, d, layers, model)
+    mcfg = CK.read_config(model)
+    assert mcfg.dims == d and abs(mcfg.scale - 0.1147213867929261) < 1e-8
+    print("[checkpoint] load_packed against fill_seeded", flush=True)
+    loaded = CK.load_packed(rt, model, d, layers=layers, head=True)
+    seeded = P.fill_seeded(rt, d, SEED, layers=layers, head=True)
+    layout = P.seeded_layout(d, layers, True)
+    assert set(loaded) == set(seeded) == set(layout)
+    for key, pt in layout.items():
+        got = loaded[key].download()
+        if pt.init == "ones":
+            assert np.array_equal(got.reshape(-1), norms[pt.source]), key
+        else:
+            assert np.array_equal(got, seeded[key].download()), key
+    for b in seeded.values():
+        b.free()
+    # the decode through run_fleet --model-dir against the oracle on the same weights and config
+    fleet = tmp_path / "fleet"
+    print(f"[checkpoint] run_fleet --model-dir layers={layers} ctx={ctx} iters={iters}", flush=True)
+    meta = RF.run(RF.build_parser().parse_args(["--model-dir", str(model), "--layers", str(layers), "--head",
+                                                "--iters", str(iters), "--ctx", str(ctx), "--out", str(fleet)]), rt=rt)
+    assert meta["completed"] and meta["softmax_scale"] == mcfg.scale
+    s_max = ctx + iters
+    plan = G.build_plan(d, s_max, layers, True, softmax_scale=mcfg.scale, eps=mcfg.eps)
+    cfg = M.Cfg(H=d.H, NH=d.NH, D_N=d.D_N, D_R=d.D_R, D_V=d.D_V, D_C=d.D_C, V=d.V, L=d.L, I_DENSE=d.I_DENSE,
+                I_MOE=d.I_MOE, E=d.E, TOPK=d.TOPK, N_SHARED=d.N_SHARED, eps=mcfg.eps, scale=mcfg.scale,
+                split=plan.split, n_splits=plan.n_splits)
+    cos, sin = mcfg.tables(s_max)
+    W = GpuWeights(loaded)
+    prompt = P.prompt_ids(SEED, ctx, d.V)
+    cache = M.Cache(cfg, s_max, layers)
+    for pos in range(ctx - 1):
+        M.decode_step(cfg, W, cache, cos, sin, prompt[pos], pos, layers, head=False)
+    ids, routes, recs = [], [], []
+    tok = int(prompt[-1])
+    for i in range(iters):
+        rec = {}
+        tok, r, _ = M.decode_step(cfg, W, cache, cos, sin, tok, ctx - 1 + i, layers, head=True, rec=rec)
+        ids.append(tok)
+        routes.append(r)
+        recs.append(rec)
+    ref = tmp_path / "ref"
+    ref.mkdir()
+    (ref / "ref_output_ids.json").write_text(json.dumps(ids))
+    (ref / "ref_route_log.json").write_text(json.dumps([[{"idx": r[:d.TOPK]} for r in step] for step in routes]))
+    BD.write(ref / "ref_boundaries_step0.safetensors", ref_boundaries(recs[0], d.TOPK))
+    BD.write(ref / f"ref_boundaries_step{iters - 1}.safetensors", ref_boundaries(recs[-1], d.TOPK))
+    res = C.run(ref, fleet, fleet / "correctness_report.md")
+    print(f"[checkpoint] fleet ids {meta['output_ids']} oracle ids {ids}: {res['overall']}", flush=True)
+    assert res["output_ids"]["result"] == "PASS", res["output_ids"]
+    assert res["route_log"]["result"] == "PASS", res["route_log"]["mismatches"][:3]
+    bad = [(r["key"], r["result"], r.get("rel_err")) for r in res["boundaries"] if r["result"] != "PASS"]
+    assert not bad and res["overall"] == "PASS", bad
+    assert all(r.get("rel_err", 0.0) == 0.0 for r in res["boundaries"])

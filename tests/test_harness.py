@@ -67,10 +67,19 @@ def test_run_writes_report(tmp_path):
     assert C.main(["--ref", str(ref), "--fleet", str(fleet)]) == 0
 
 
-def test_run_fleet_refuses_checkpoint_and_bad_args(tmp_path):
+def test_run_fleet_refuses_bad_model_dirs_and_args(tmp_path):
     ap = RF.build_parser()
-    with pytest.raises(SystemExit, match="checkpoint loader"):
-        RF.run(ap.parse_args(["--model-dir", "/nonexistent", "--out", str(tmp_path)]))
+    with pytest.raises(SystemExit, match="no config.json"):
+        RF.run(ap.parse_args(["--model-dir", str(tmp_path / "nonexistent"), "--out", str(tmp_path)]))
+    other = tmp_path / "other"
+    other.mkdir()
+    (other / "config.json").write_text(json.dumps({
+        "hidden_size": 4096, "num_attention_heads": 16, "qk_nope_head_dim": 128, "qk_rope_head_dim": 64,
+        "v_head_dim": 128, "kv_lora_rank": 512, "vocab_size": 102400, "num_hidden_layers": 27,
+        "intermediate_size": 10944, "moe_intermediate_size": 1408, "n_routed_experts": 64,
+        "num_experts_per_tok": 6, "n_shared_experts": 2}))
+    with pytest.raises(SystemExit, match="built for DeepSeek-V2-Lite"):
+        RF.run(ap.parse_args(["--model-dir", str(other), "--out", str(tmp_path)]))
     with pytest.raises(SystemExit, match="--layers"):
         RF.run(ap.parse_args(["--layers", "28", "--out", str(tmp_path)]))
     with pytest.raises(SystemExit, match="--iters"):
