@@ -5,15 +5,17 @@ the HBM roofline, on one MI355X.
 Workload: the full 27-layer DeepSeek-V2-Lite with random-init bf16 weights
 ~N(0, 0.02) from a seed (norm weights 1.0), a 1,024-token prompt drawn uniformly from the 102,400-id
 vocabulary with a seed, an untimed prefill that writes the latent caches of positions 0..1022
-through the same persistent kernel (teacher-forced iterations, head skipped), then greedy decode
-at batch 1. A "step" is one decoded token; `--steps` tokens are timed, starting at position 1023
+(--prefill batched, the default: one forward pass over all prompt positions, fleet/prefill.py;
+--prefill decode: teacher-forced iterations of the persistent kernel, head skipped), then greedy
+decode at batch 1. A "step" is one decoded token; `--steps` tokens are timed, starting at position 1023
 (so every timed token attends over 1,024..1,024+steps-1 positions), after `--warmup` untimed
 tokens at the same positions. Inputs are resident in HBM when the timed region starts.
 
 value        us per decoded token: one persistent launch per token (fx_launch, queued back to back on
              one stream, no host wait in between); HIP events on that stream around the K launches
-             / K. Prefill runs under the kernel symbol fx_prefill, decode under fx_persistent, so a
-             kernel trace of this command averages fx_persistent over decode tokens only
+             / K. Decode runs under the kernel symbol fx_persistent (a --prefill decode prefill under
+             fx_prefill, the batched one in rocBLAS and fx_pf_* kernels), so a kernel trace of this
+             command averages fx_persistent over decode tokens only
 roofline     algorithmic HBM bytes per token (every weight the token touches once -- 8 of the 66
              experts per MoE layer -- plus the latent-cache rows read and the embedding row; mean
              over the timed tokens) / us per token, against the published 8 TB/s; traffic = the
@@ -40,6 +42,7 @@ import numpy as np  # noqa: E402
 from fleet import build_graph as B  # noqa: E402
 from fleet import graph_plan as G  # noqa: E402
 from fleet import pack_weights as P  # noqa: E402
+from fleet import prefill as PF  # noqa: E402
 from fleet import runtime as R  # noqa: E402
 
 HBM_PEAK_GBPS = 8000.0
@@ -126,6 +129,8 @@ def main():
     ap.add_argument("--cpu-tokens", type=int, default=16)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--n-splits", type=int, default=None, help="attention splits (default: 32-position splits)")
+    ap.add_argument("--prefill", choices=("batched", "decode"), default="batched",
+                    help="how the untimed prefill writes the caches (batched forward pass or the decode kernel)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (this build has no multi-GPU path; --gpus {args.gpus} is not "
@@ -151,9 +156,21 @@ def main():
     runner = B.build(rt, bufs, cap, meta, d, s_max, d.L, True)
     log(f"plan: {len(runner.stages)} stages/iteration, {plan.n_splits} splits of {plan.split}, s_max {s_max}")
     t0 = time.time()
-    runner.run(ctx - 1, 0, ctx)
-    prefill_s = time.time() - t0
-    log(f"prefill of {ctx - 1} positions: {prefill_s:.2f} s ({1e6 * prefill_s / (ctx - 1):.0f} us/position, head skipped)")
+    prefill_warm_s = None
+    if args.prefill == "batched":
+        pf = PF.Prefill(rt, bufs, runner.host, d, ctx, d.L, plan.eps, plan.scale, G.ROUTED_SCALING)
+        pf.run(runner.host["tokens"])
+        prefill_s = time.time() - t0
+        # again, past rocBLAS's one-time kernel loading (the same inputs write the same rows)
+        t1 = time.time()
+        pf.run(runner.host["tokens"])
+        prefill_warm_s = time.time() - t1
+        pf.free()
+    else:
+        runner.run(ctx - 1, 0, ctx)
+        prefill_s = time.time() - t0
+    log(f"{args.prefill} prefill of {ctx - 1} positions: {prefill_s:.2f} s"
+        + (f", {prefill_warm_s:.3f} s once the GEMM kernels are loaded" if prefill_warm_s else ""))
     assert K + 1 <= R.FX_MAX_MARKS, "at most 255 timed tokens"
     for i in range(Wm):
         runner.launch(1, ctx - 1 + i, ctx)
@@ -186,7 +203,8 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic_bytes(ctx),
                      "bytes_per_token": int(mean_bytes), "kernel": "fx_persistent"},
-        "launch_us_median": round(statistics.median(per_launch), 2), "prefill_s": round(prefill_s, 2),
+        "launch_us_median": round(statistics.median(per_launch), 2), "prefill": args.prefill,
+        "prefill_s": round(prefill_s, 3), "prefill_warm_s": None if prefill_warm_s is None else round(prefill_warm_s, 3),
         "ids": ids,
     }
     if not args.no_cpu_baseline:

@@ -20,6 +20,9 @@
 #include <vector>
 
 #include "fx_ops.h"
+#include "fx_prefill.h"
+
+#include <rocblas/rocblas.h>
 
 #define FX_BLOCKS 256
 static_assert(sizeof(fx_stage) == 208, "fx_stage layout is part of the ABI (fleet/runtime.py FxStage)");
@@ -251,6 +254,7 @@ struct fx_ctx {
   uint64_t* prof = nullptr;
   size_t prof_words = 0;
   int prof_iter = -1;
+  rocblas_handle blas = nullptr;   // the prefill's GEMMs (created on first use)
 };
 
 static int fail(fx_ctx* c, int code, const std::string& msg) {
@@ -321,6 +325,7 @@ int fx_destroy(fx_ctx* c) {
   for (hipEvent_t e : c->marks)
     if (e) (void)hipEventDestroy(e);
   if (c->prof) (void)hipFree(c->prof);
+  if (c->blas) (void)rocblas_destroy_handle(c->blas);
   delete c;
   return FX_OK;
 }
@@ -646,6 +651,146 @@ int fx_fill_u16(fx_ctx* c, void* dst, uint64_t n, uint16_t v) {
   uint64_t grid = (n + 255) / 256;
   if (grid > 65536) grid = 65536;
   hipLaunchKernelGGL(fx_fill_kernel, dim3((unsigned)grid), dim3(256), 0, 0, (uint16_t*)dst, n, v);
+  HIPCHK(c, hipGetLastError());
+  return FX_OK;
+}
+
+// ------------------------------------------------------------------------------------------------
+// batched prefill: rocBLAS GEMMs and the row kernels of fx_prefill.h
+
+#define PF_CHECK(c, cond, msg) \
+  do {                         \
+    if (!(cond)) return fail((c), FX_E_ARG, msg); \
+  } while (0)
+
+static bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+int fx_gemm(fx_ctx* c, int32_t trans_a, int32_t trans_b, int32_t M, int32_t N, int32_t K, float alpha, const void* A,
+            int64_t lda, int64_t stride_a, const void* B, int64_t ldb, int64_t stride_b, float beta, const void* C,
+            int64_t ldc, int64_t stride_c, void* D, int64_t ldd, int64_t stride_d, int32_t d_f32, int32_t batch,
+            void* stream) {
+  if (!c) return FX_E_ARG;
+  PF_CHECK(c, M > 0 && N > 0 && K > 0 && batch > 0, "fx_gemm: empty shape");
+  PF_CHECK(c, A && B && D && (beta == 0.0f || C), "fx_gemm: null operand");
+  PF_CHECK(c, lda >= (trans_a ? M : K) && ldb >= (trans_b ? K : N) && ldd >= N && (beta == 0.0f || ldc >= N),
+           "fx_gemm: leading dimension smaller than the row");
+  if (!c->blas) {
+    if (rocblas_create_handle(&c->blas) != rocblas_status_success) return fail(c, FX_E_HIP, "rocblas_create_handle");
+  }
+  if (rocblas_set_stream(c->blas, (hipStream_t)stream) != rocblas_status_success)
+    return fail(c, FX_E_HIP, "rocblas_set_stream");
+  // row-major D[M,N] = op(A) op(B) is column-major D^T[N,M] = op(B)^T op(A)^T: B first
+  const rocblas_datatype dt = d_f32 ? rocblas_datatype_f32_r : rocblas_datatype_bf16_r;
+  rocblas_status st = rocblas_gemm_strided_batched_ex(
+      c->blas, trans_b ? rocblas_operation_transpose : rocblas_operation_none,
+      trans_a ? rocblas_operation_transpose : rocblas_operation_none, N, M, K, &alpha, B, rocblas_datatype_bf16_r, ldb,
+      stride_b, A, rocblas_datatype_bf16_r, lda, stride_a, &beta, beta == 0.0f ? D : C, dt, beta == 0.0f ? ldd : ldc,
+      beta == 0.0f ? stride_d : stride_c, D, dt, ldd, stride_d, batch, rocblas_datatype_f32_r, rocblas_gemm_algo_standard,
+      0, 0);
+  if (st != rocblas_status_success)
+    return fail(c, FX_E_HIP, std::string("rocblas_gemm_strided_batched_ex: ") + rocblas_status_to_string(st));
+  return FX_OK;
+}
+
+int fx_pf_embed(fx_ctx* c, const int64_t* tokens, const void* W, void* x, int32_t M, int32_t H, void* stream) {
+  if (!c) return FX_E_ARG;
+  PF_CHECK(c, tokens && W && x && M > 0 && H > 0 && H % 8 == 0 && al16(W) && al16(x), "fx_pf_embed: arguments");
+  hipLaunchKernelGGL(pf_embed_kernel, dim3(M), dim3(PF_THREADS), 0, (hipStream_t)stream, tokens, (const uint16_t*)W,
+                     (uint16_t*)x, H);
+  HIPCHK(c, hipGetLastError());
+  return FX_OK;
+}
+
+int fx_pf_rmsnorm(fx_ctx* c, const void* x, int64_t ldx, const void* w, void* y, int64_t ldy, int32_t M, int32_t K,
+                  float eps, void* stream) {
+  if (!c) return FX_E_ARG;
+  PF_CHECK(c, x && w && y && M > 0 && K > 0 && K % 8 == 0 && K <= 16384 && ldx >= K && ldy >= K && ldx % 8 == 0 &&
+                  ldy % 8 == 0 && al16(x) && al16(y) && al16(w),
+           "fx_pf_rmsnorm: arguments");
+  const size_t lds = (size_t)(((K + 63) & ~63) + 64) * 4;
+  hipLaunchKernelGGL(pf_rmsnorm_kernel, dim3(M), dim3(PF_THREADS), lds, (hipStream_t)stream, (const uint16_t*)x, ldx,
+                     (const uint16_t*)w, (uint16_t*)y, ldy, K, eps);
+  HIPCHK(c, hipGetLastError());
+  return FX_OK;
+}
+
+int fx_pf_prep(fx_ctx* c, const void* qkva, int64_t ldq, const void* w_kv_norm, const void* cos, const void* sin,
+               void* c_kv, void* k_pe, void* q_pe, int32_t pos0, int32_t M, int32_t s_max, int32_t n_heads,
+               int32_t d_n, int32_t d_c, float eps, void* stream) {
+  if (!c) return FX_E_ARG;
+  PF_CHECK(c, qkva && w_kv_norm && cos && sin && c_kv && k_pe && q_pe && M > 0 && pos0 >= 0 && pos0 + M <= s_max &&
+                  n_heads > 0 && n_heads <= 64 && d_n > 0 && d_c > 0 && d_c % 8 == 0 && d_c <= 4096 &&
+                  ldq >= (int64_t)n_heads * (d_n + 64) + d_c + 64 && al16(w_kv_norm),
+           "fx_pf_prep: arguments");
+  const size_t lds = (size_t)(d_c + (1 + n_heads) * 64 + 64) * 4;
+  hipLaunchKernelGGL(pf_prep_kernel, dim3(M), dim3(PF_THREADS), lds, (hipStream_t)stream, (const uint16_t*)qkva, ldq,
+                     (const uint16_t*)w_kv_norm, (const uint16_t*)cos, (const uint16_t*)sin, (uint16_t*)c_kv,
+                     (uint16_t*)k_pe, (uint16_t*)q_pe, pos0, n_heads, d_n, d_c, eps);
+  HIPCHK(c, hipGetLastError());
+  return FX_OK;
+}
+
+int fx_pf_softmax(fx_ctx* c, const void* S, int64_t ldS, int64_t strideS, void* P, int64_t ldP, int64_t strideP,
+                  void* l, int64_t strideL, int32_t M, int32_t heads, int32_t n_cols, int32_t key0, float scale,
+                  void* stream) {
+  if (!c) return FX_E_ARG;
+  PF_CHECK(c, S && P && l && M > 0 && heads > 0 && heads <= 65535 && n_cols > 0 && key0 >= 0 && ldS >= n_cols &&
+                  ldP >= n_cols && strideL >= M,
+           "fx_pf_softmax: arguments");
+  hipLaunchKernelGGL(pf_softmax_kernel, dim3(M, heads), dim3(PF_THREADS), 0, (hipStream_t)stream, (const float*)S, ldS,
+                     strideS, (uint16_t*)P, ldP, strideP, (float*)l, strideL, n_cols, key0, scale);
+  HIPCHK(c, hipGetLastError());
+  return FX_OK;
+}
+
+int fx_pf_attn_out(fx_ctx* c, const void* O, const void* l, void* obf, int32_t M, int32_t heads, int32_t d,
+                   void* stream) {
+  if (!c) return FX_E_ARG;
+  PF_CHECK(c, O && l && obf && M > 0 && heads > 0 && heads <= 65535 && d > 0, "fx_pf_attn_out: arguments");
+  hipLaunchKernelGGL(pf_attn_out_kernel, dim3(M, heads), dim3(PF_THREADS), 0, (hipStream_t)stream, (const float*)O,
+                     (const float*)l, (uint16_t*)obf, M, d);
+  HIPCHK(c, hipGetLastError());
+  return FX_OK;
+}
+
+int fx_pf_silu(fx_ctx* c, const void* gu, void* act, int32_t rows, int32_t I, void* stream) {
+  if (!c) return FX_E_ARG;
+  PF_CHECK(c, gu && act && rows >= 0 && I > 0, "fx_pf_silu: arguments");
+  if (rows == 0) return FX_OK;
+  hipLaunchKernelGGL(pf_silu_kernel, dim3(rows), dim3(PF_THREADS), 0, (hipStream_t)stream, (const uint16_t*)gu,
+                     (uint16_t*)act, I);
+  HIPCHK(c, hipGetLastError());
+  return FX_OK;
+}
+
+int fx_pf_route(fx_ctx* c, const void* logits, void* ids, void* wts, int32_t M, int32_t E, int32_t topk,
+                int32_t n_shared, float scaling, void* stream) {
+  if (!c) return FX_E_ARG;
+  PF_CHECK(c, logits && ids && wts && M > 0 && E > 0 && E <= 64 && topk > 0 && topk <= E && n_shared >= 0 &&
+                  topk + n_shared <= 16,
+           "fx_pf_route: arguments");
+  hipLaunchKernelGGL(pf_route_kernel, dim3(M), dim3(64), 0, (hipStream_t)stream, (const float*)logits, E, topk,
+                     n_shared, scaling, (int32_t*)ids, (float*)wts);
+  HIPCHK(c, hipGetLastError());
+  return FX_OK;
+}
+
+int fx_pf_gather(fx_ctx* c, const void* src, const void* idx, void* dst, int32_t rows, int32_t H, void* stream) {
+  if (!c) return FX_E_ARG;
+  PF_CHECK(c, src && idx && dst && rows >= 0 && H > 0 && H % 8 == 0 && al16(src) && al16(dst), "fx_pf_gather: arguments");
+  if (rows == 0) return FX_OK;
+  hipLaunchKernelGGL(pf_gather_kernel, dim3(rows), dim3(PF_THREADS), 0, (hipStream_t)stream, (const uint16_t*)src,
+                     (const int32_t*)idx, (uint16_t*)dst, H);
+  HIPCHK(c, hipGetLastError());
+  return FX_OK;
+}
+
+int fx_pf_combine(fx_ctx* c, const void* x_mid, const void* og, const void* inv, const void* w, void* x_res, int32_t M,
+                  int32_t H, int32_t slots, void* stream) {
+  if (!c) return FX_E_ARG;
+  PF_CHECK(c, x_mid && og && inv && w && x_res && M > 0 && H > 0 && slots > 0, "fx_pf_combine: arguments");
+  hipLaunchKernelGGL(pf_combine_kernel, dim3(M), dim3(PF_THREADS), 0, (hipStream_t)stream, (const uint16_t*)x_mid,
+                     (const uint16_t*)og, (const int32_t*)inv, (const float*)w, (uint16_t*)x_res, H, slots);
   HIPCHK(c, hipGetLastError());
   return FX_OK;
 }

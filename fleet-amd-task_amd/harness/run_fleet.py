@@ -10,9 +10,11 @@ What differs from the reference, and why:
     plain RoPE, scale 192^-0.5); with it, the checkpoint's safetensors shards are loaded into the
     same packed keys (fleet/checkpoint.py) and the config's YaRN tables, softmax scale and norm eps
     are used;
-  * the prompt's cache rows 0 .. n_prompt - 2 are produced by this kernel itself (teacher-forced
-    iterations, head skipped) instead of being captured from the HF prefill (--ref's
-    ref_cache.safetensors), so the whole run is one fx_run over positions 0 .. n_prompt - 2 + iters;
+  * the prompt's cache rows 0 .. n_prompt - 2 are produced on the GPU instead of being captured from
+    the HF prefill (--ref's ref_cache.safetensors): by default by the decode kernel itself
+    (teacher-forced iterations, head skipped; the whole run is one fx_run over positions
+    0 .. n_prompt - 2 + iters), with --prefill batched by one forward pass over all prompt positions
+    (fleet/prefill.py: rocBLAS GEMMs + this library's row kernels), then fx_run from n_prompt - 1;
   * there is no compile step (fx_load_plan validates and uploads the task table).
 
 Files written to --out (the reference's names and formats):
@@ -41,6 +43,7 @@ from fleet import build_graph as B  # noqa: E402
 from fleet import graph_plan as G  # noqa: E402
 from fleet import pack_weights as P  # noqa: E402
 from fleet import checkpoint as CK  # noqa: E402
+from fleet import prefill as PF  # noqa: E402
 from fleet import runtime as R  # noqa: E402
 
 sys.path.insert(0, str(Path(__file__).resolve().parent))
@@ -63,6 +66,9 @@ def build_parser():
     ap.add_argument("--n-splits", type=int, default=None, help="attention split count (default: at most 32)")
     ap.add_argument("--out", default=None, help="run directory (default: harness/fleet_out/<name>)")
     ap.add_argument("--event-timing", action="store_true", help="per-stage stamps of the last iteration")
+    ap.add_argument("--prefill", choices=("decode", "batched"), default="decode",
+                    help="decode: the prompt positions run through the decode kernel (teacher-forced, bit-exact "
+                         "with the oracle); batched: one forward pass over all prompt positions (fleet/prefill.py)")
     ap.add_argument("--final", action="store_true", help="accepted for the reference's command line; this build "
                                                          "has one configuration")
     ap.add_argument("--model-dir", default=None, help="HF snapshot directory (config.json + safetensors shards); "
@@ -144,11 +150,20 @@ def run(args, rt=None):
         (out / "fleet_run_meta.json").write_text(json.dumps(meta_out, indent=2) + "\n")
         total = n_prompt - 1 + args.iters
         t2 = time.time()
+        t_prefill = None
+        step0, n_iter = 0, total
+        if args.prefill == "batched":
+            pf = PF.Prefill(rt, packed, runner.host, d, n_prompt, layers, runner.plan.eps, runner.plan.scale,
+                            G.ROUTED_SCALING)
+            pf.run(runner.host["tokens"])
+            pf.free()
+            t_prefill = time.time() - t2
+            step0, n_iter = n_prompt - 1, args.iters
         if args.event_timing:
-            rows = runner.profile(total, 0, n_prompt, iteration=total - 1)
+            rows = runner.profile(n_iter, step0, n_prompt, iteration=n_iter - 1)
             (out / "event_timing.json").write_text(json.dumps(rows) + "\n")
         else:
-            runner.run(total, 0, n_prompt)
+            runner.run(n_iter, step0, n_prompt)
         t_run = time.time() - t2
         ids = runner.host["tokens"].download()[n_prompt:n_prompt + args.iters].tolist()
         if not args.head or args.stop_after:
@@ -161,7 +176,8 @@ def run(args, rt=None):
         bnd, notes = BD.dump(pj["calls"], runner.host, n_prompt, d.TOPK, d.Q_OUT, args.iters)
         BD.write(out / "fleet_boundaries.safetensors", bnd, {"iters": args.iters, "n_prompt": n_prompt})
         meta_out.update({"boundaries": sorted(bnd), "boundary_notes": notes})
-        wall = {"run_wall_s": t_run, "iters": args.iters, "positions": total, "pack_s": t_pack, "build_s": t_build}
+        wall = {"run_wall_s": t_run, "iters": args.iters, "positions": total, "pack_s": t_pack, "build_s": t_build,
+                "prefill": args.prefill, "prefill_s": t_prefill}
         (out / "wall.json").write_text(json.dumps(wall) + "\n")
         meta_out.update({"output_ids": ids, "timings_s": wall, "completed": True})
         (out / "fleet_run_meta.json").write_text(json.dumps(meta_out, indent=2) + "\n")

@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define FX_ABI_VERSION 3
+#define FX_ABI_VERSION 4
 
 /* ---- error codes ---------------------------------------------------------------------------- */
 #define FX_OK 0
@@ -221,6 +221,52 @@ int fx_time_stages(fx_ctx* ctx, const fx_stage* stages, int32_t n, int32_t reps,
 int fx_gen_normal_bf16(fx_ctx* ctx, void* dst, uint64_t rows, uint64_t row_len, uint64_t dst_stride,
                        uint64_t src_offset, uint64_t src_stride, uint64_t seed, uint32_t stream, float scale);
 int fx_fill_u16(fx_ctx* ctx, void* dst, uint64_t n, uint16_t value);
+
+/* ---- batched prefill (fleet/prefill.py) ------------------------------------------------------- */
+/* The prompt's forward pass over M positions at once, writing the latent-cache rows the decode
+ * consumes. The reference has no prefill of its own: it captures the caches from the HF model's
+ * prefill (harness/run_reference.py:367-376, 414-425; run_fleet.py:533-537 uploads them). Plain
+ * GEMMs go to rocBLAS; the row work between them is this library's kernels, rounding at the
+ * decode spec's points. All launches are asynchronous on `stream`. */
+
+/* Row-major D[b] = alpha * op(A[b]) op(B[b]) + beta * C[b] for b < batch: A, B bf16, FP32 accumulate,
+ * C and D bf16 (d_f32 = 0) or FP32 (d_f32 = 1); op(X) = X^T when trans_x. op(A) is [M, K] (A stored
+ * [M, lda] or, transposed, [K, lda]), op(B) is [K, N] (B stored [K, ldb] or, transposed, [N, ldb]);
+ * strides in elements between batch entries; C may equal D. */
+int fx_gemm(fx_ctx* ctx, int32_t trans_a, int32_t trans_b, int32_t M, int32_t N, int32_t K, float alpha,
+            const void* A, int64_t lda, int64_t stride_a, const void* B, int64_t ldb, int64_t stride_b, float beta,
+            const void* C, int64_t ldc, int64_t stride_c, void* D, int64_t ldd, int64_t stride_d, int32_t d_f32,
+            int32_t batch, void* stream);
+/* x[m] = W_embed[tokens[m]] (H bf16 per row). */
+int fx_pf_embed(fx_ctx* ctx, const int64_t* tokens, const void* W_embed, void* x, int32_t M, int32_t H, void* stream);
+/* y[m] = rmsnorm(x[m]) * w (K bf16 per row at strides ldx / ldy elements; numpy_ref.py:54-60). */
+int fx_pf_rmsnorm(fx_ctx* ctx, const void* x, int64_t ldx, const void* w, void* y, int64_t ldy, int32_t M, int32_t K,
+                  float eps, void* stream);
+/* MLA prep of rows m < M at positions pos0 + m (numpy_ref.py:85-103): c_kv[pos] = rmsnorm of the
+ * latent, k_pe[pos] = RoPE of the rope part (both caches [s_max, .]), q_pe[m][h] = RoPE of q's rope
+ * part ([M, n_heads, 64]); qkva rows [n_heads * (d_n + 64) + d_c + 64] at stride ldq. */
+int fx_pf_prep(fx_ctx* ctx, const void* qkva, int64_t ldq, const void* w_kv_norm, const void* cos, const void* sin,
+               void* c_kv, void* k_pe, void* q_pe, int32_t pos0, int32_t M, int32_t s_max, int32_t n_heads,
+               int32_t d_n, int32_t d_c, float eps, void* stream);
+/* Causal softmax of FP32 score rows i < M of `heads` heads: keys j <= key0 + i (of n_cols);
+ * P = bf16(exp(S * scale - max)) (0 past the last key), l = the FP32 sum. */
+int fx_pf_softmax(fx_ctx* ctx, const void* S, int64_t ldS, int64_t strideS, void* P, int64_t ldP, int64_t strideP,
+                  void* l, int64_t strideL, int32_t M, int32_t heads, int32_t n_cols, int32_t key0, float scale,
+                  void* stream);
+/* obf[h][i][c] = bf16(O[h][i][c] / l[h][i]) (O FP32 [heads, M, d]). */
+int fx_pf_attn_out(fx_ctx* ctx, const void* O, const void* l, void* obf, int32_t M, int32_t heads, int32_t d,
+                   void* stream);
+/* act[r][i] = bf16(silu(gu[r][i]) * gu[r][I + i]) (numpy_ref.py:248-253, 262-272). */
+int fx_pf_silu(fx_ctx* ctx, const void* gu, void* act, int32_t rows, int32_t I, void* stream);
+/* Router of each row (numpy_ref.py:216-227): ids [M, topk + n_shared] = top-k of softmax(logits),
+ * then the shared experts E.., wts = p * scaling, then 1.0 (logits FP32 [M, E]). */
+int fx_pf_route(fx_ctx* ctx, const void* logits, void* ids, void* wts, int32_t M, int32_t E, int32_t topk,
+                int32_t n_shared, float scaling, void* stream);
+/* dst[r] = src[idx[r]] (rows of H bf16). */
+int fx_pf_gather(fx_ctx* ctx, const void* src, const void* idx, void* dst, int32_t rows, int32_t H, void* stream);
+/* x_res[m] = bf16(x_mid[m] + sum_s og[inv[m][s]] * w[m][s]) in slot order (numpy_ref.py:316-321). */
+int fx_pf_combine(fx_ctx* ctx, const void* x_mid, const void* og, const void* inv, const void* w, void* x_res,
+                  int32_t M, int32_t H, int32_t slots, void* stream);
 
 #ifdef __cplusplus
 }

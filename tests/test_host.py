@@ -26,7 +26,7 @@ def test_library_exports_every_declared_symbol():
     lib = ctypes.CDLL(str(R.LIB_PATH))
     for name in declared:
         assert hasattr(lib, name), name
-    assert R.lib().fx_abi_version() == R.FX_ABI_VERSION == 3
+    assert R.lib().fx_abi_version() == R.FX_ABI_VERSION == 4
 
 
 def test_stage_struct_size_matches_header():
