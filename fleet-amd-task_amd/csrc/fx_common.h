@@ -39,7 +39,10 @@ __device__ __forceinline__ void prof_mark(const FxEnv& e, int slot) {
 #define LDS_MISC (LDS_RED + 4096)        // scalars: token, expert, slot weights
 #define LDS_RES (LDS_MISC + 512)         // f32 [128]    residual / output values of the worker's rows
 #define LDS_TILE (LDS_MISC + 1024)       // attention tile / merge tables (<= 37.5 KiB)
-#define LDS_STAGE (FX_LDS_BYTES - 256)   // the current fx_stage (persistent kernel)
+#define LDS_STAGE (FX_LDS_BYTES - 256)   // end of the operators' LDS (the last 256 B unused)
+// the persistent kernel's task table (every stage, then the epilogue) past the operators' LDS
+#define FX_TABLE_MAX 300
+#define FX_LDS_TOTAL (FX_LDS_BYTES + FX_TABLE_MAX * 208)
 #define FX_MAX_OUT_ROWS 128
 
 __device__ __forceinline__ void range_split(int n, int parts, int i, int& lo, int& hi) {

@@ -64,13 +64,15 @@ __device__ __forceinline__ void persistent_body(const FxRunArgs& a) {
   const int b = blockIdx.x;
   FxEnv env;
   env_init(env, lds, a.tokens, a.err, a.n_prompt);
-  // the current stage descriptor is staged in LDS (read by every wave, never spilled to scratch)
-  fx_stage* sst = (fx_stage*)(lds + LDS_STAGE);
-  auto stage_in = [&](const fx_stage* src) {
-    __syncthreads();
-    if (threadIdx.x < sizeof(fx_stage) / 4) ((uint32_t*)sst)[threadIdx.x] = ((const uint32_t*)src)[threadIdx.x];
-    __syncthreads();
-  };
+  // the task table (stages, then the epilogue) is copied into LDS once per launch: a stage starts
+  // with one barrier (the operators reuse the same LDS regions) and reads its descriptor from LDS
+  fx_stage* table = (fx_stage*)(lds + FX_LDS_BYTES);
+  {
+    const int w0 = a.n_stages * (int)(sizeof(fx_stage) / 16), w1 = a.n_epi * (int)(sizeof(fx_stage) / 16);
+    u32x4* dst = (u32x4*)table;
+    for (int i = threadIdx.x; i < w0; i += FX_THREADS) dst[i] = ld16((const u32x4*)a.stages + i);
+    for (int i = threadIdx.x; i < w1; i += FX_THREADS) dst[w0 + i] = ld16((const u32x4*)a.epi + i);
+  }
   for (int it = 0; it < a.iters; ++it) {
     env.iter = it;
     env.step = a.step0 + it;
@@ -79,7 +81,8 @@ __device__ __forceinline__ void persistent_body(const FxRunArgs& a) {
     if (b == 0 && threadIdx.x == 0 && a.timing) a.timing[it] = __builtin_amdgcn_s_memrealtime();
     const bool prof = a.prof && it == a.prof_iter;
     for (int s = 0; s < a.n_stages; ++s) {
-      stage_in(a.stages + s);
+      __syncthreads();
+      const fx_stage* sst = table + s;
       if ((sst->flags & FX_F_HEAD) && (env.step + 1 < env.n_prompt)) continue;
       env.sidx = s;
       env.pst = prof ? a.prof + ((size_t)s * FX_BLOCKS + b) * FX_PROF_SLOTS : nullptr;
@@ -96,9 +99,9 @@ __device__ __forceinline__ void persistent_body(const FxRunArgs& a) {
   env.step = a.step0 + a.iters - 1;
   env.tbase = a.epoch0 + (uint32_t)(a.iters * a.n_stages);
   for (int s = 0; s < a.n_epi; ++s) {
-    stage_in(a.epi + s);
+    __syncthreads();
     env.sidx = a.n_stages + s;
-    run_stage(*sst, env);
+    run_stage(table[a.n_stages + s], env);
   }
   if (b == 0 && threadIdx.x == 0 && a.timing) a.timing[a.iters] = __builtin_amdgcn_s_memrealtime();
 }
@@ -284,14 +287,14 @@ int fx_create(int device, fx_ctx** out) {
   if (hipGetDeviceProperties(&pr, device) != hipSuccess) { delete c; return FX_E_HIP; }
   c->cus = pr.multiProcessorCount;
   if (std::strncmp(pr.gcnArchName, "gfx950", 6) != 0 || pr.multiProcessorCount != FX_BLOCKS ||
-      pr.sharedMemPerBlock < (size_t)FX_LDS_BYTES) {
+      pr.sharedMemPerBlock < (size_t)FX_LDS_TOTAL) {
     *out = c;
     return fail(c, FX_E_DEVICE, std::string("expected a gfx950 with 256 CUs, got ") + pr.gcnArchName + " with " +
                                     std::to_string(pr.multiProcessorCount) + " CUs");
   }
   *out = c;
-  HIPCHK(c, hipFuncSetAttribute((const void*)fx_persistent, hipFuncAttributeMaxDynamicSharedMemorySize, FX_LDS_BYTES));
-  HIPCHK(c, hipFuncSetAttribute((const void*)fx_prefill, hipFuncAttributeMaxDynamicSharedMemorySize, FX_LDS_BYTES));
+  HIPCHK(c, hipFuncSetAttribute((const void*)fx_persistent, hipFuncAttributeMaxDynamicSharedMemorySize, FX_LDS_TOTAL));
+  HIPCHK(c, hipFuncSetAttribute((const void*)fx_prefill, hipFuncAttributeMaxDynamicSharedMemorySize, FX_LDS_TOTAL));
   HIPCHK(c, hipFuncSetAttribute((const void*)fx_stage_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, FX_LDS_BYTES));
   HIPCHK(c, hipFuncSetAttribute((const void*)fx_xcc_map, hipFuncAttributeMaxDynamicSharedMemorySize, FX_LDS_BYTES));
   HIPCHK(c, hipMalloc(&c->err_flag, FX_ERR_WORDS * 4));
@@ -443,6 +446,9 @@ static int check_stage(fx_ctx* c, const fx_stage& s, int idx, int n_total) {
 int fx_load_plan(fx_ctx* c, const fx_stage* st, int32_t n, const fx_stage* epi, int32_t n_epi) {
   if (!c) return FX_E_ARG;
   if (n <= 0 || !st) return fail(c, FX_E_ARG, "empty plan");
+  if (n_epi < 0 || n + n_epi > FX_TABLE_MAX)
+    return fail(c, FX_E_ARG, "the plan has " + std::to_string(n) + " stages + " + std::to_string(n_epi) +
+                                 " epilogue stages; the persistent kernel holds at most " + std::to_string(FX_TABLE_MAX));
   for (int i = 0; i < n; ++i) {
     int r = check_stage(c, st[i], i, n);
     if (r) return r;
@@ -508,7 +514,7 @@ int fx_launch(fx_ctx* c, int32_t iters, int32_t step0, int32_t n_prompt, int64_t
   const bool prefill = (int64_t)step0 + iters < (int64_t)n_prompt;
   const void* fn = prefill ? (const void*)fx_prefill : (const void*)fx_persistent;
   HIPCHK(c, hipEventRecord(c->ev0, s));
-  HIPCHK(c, hipLaunchCooperativeKernel(fn, dim3(FX_BLOCKS), dim3(FX_THREADS), args, FX_LDS_BYTES, s));
+  HIPCHK(c, hipLaunchCooperativeKernel(fn, dim3(FX_BLOCKS), dim3(FX_THREADS), args, FX_LDS_TOTAL, s));
   HIPCHK(c, hipEventRecord(c->ev1, s));
   c->epoch += (uint32_t)total;
   c->last_iters = iters;
