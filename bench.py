@@ -90,17 +90,31 @@ def cpu_baseline(rt, runner, bufs, plan, prompt, ctx, n_tok, gpu_ids):
     W["W_gu_0"], W["W_down_0"] = bufs["W_gu_0"].download(), bufs["W_down_0"].download()
     rl = runner.host["route_log"].download()
     experts = {}
+    fp8 = plan.fp8_experts
     for l in range(1, d.L):
         W[f"W_gate_{l}"] = bufs[f"W_gate_{l}"].download()
         for i in range(n_tok):
             for e in rl[i, l - 1].tolist():
+                if fp8:
+                    for key, rows, K in ((f"W13q_{l}", 2 * d.I_MOE, d.H), (f"W2q_{l}", d.H, d.I_MOE)):
+                        if (key, e) not in experts:
+                            buf = bufs[key]
+                            q = buf.download_range(e * rows * K, rows * K).reshape(rows, K)
+                            sc = buf.download_range(d.E_TOTAL * rows * K + 4 * e * rows, 4 * rows).view(np.float32)
+                            experts[(key, e)] = (q, sc)
+                    continue
                 for key, per in ((f"W13_{l}", 2 * d.I_MOE * d.H), (f"W2_{l}", d.H * d.I_MOE)):
                     if (key, e) not in experts:
                         shape = bufs[key].shape[1:]
                         experts[(key, e)] = bufs[key].download_range(e * per, per).reshape(shape)
 
     class HostW(dict):
+        fp8_experts = fp8
+
         def expert(self, key, e):
+            return experts[(key, e)]
+
+        def fp8_expert(self, key, e, rows, K):
             return experts[(key, e)]
 
     Wh = HostW(W)
@@ -129,6 +143,8 @@ def main():
     ap.add_argument("--cpu-tokens", type=int, default=16)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--n-splits", type=int, default=None, help="attention splits (default: 32-position splits)")
+    ap.add_argument("--fp8-experts", action="store_true",
+                    help="the experts' weights as FP8 (weight-only e4m3, per-row scales) instead of bf16")
     ap.add_argument("--prefill", choices=("batched", "decode"), default="batched",
                     help="how the untimed prefill writes the caches (batched forward pass or the decode kernel)")
     args = ap.parse_args()
@@ -150,10 +166,14 @@ def main():
     gen_s = time.time() - t0
     log(f"seeded weights: {P.packed_bytes(d) / 2**30:.2f} GiB in {gen_s:.1f} s")
     prompt = P.prompt_ids(args.seed, ctx, d.V)
-    plan = G.build_plan(d, s_max, d.L, True, n_splits=args.n_splits)
+    if args.fp8_experts:
+        t0 = time.time()
+        P.quantize_experts(rt, bufs, d, d.L)
+        log(f"FP8 experts: quantized in {time.time() - t0:.1f} s")
+    plan = G.build_plan(d, s_max, d.L, True, n_splits=args.n_splits, fp8_experts=args.fp8_experts)
     meta = B.make_meta(rt, s_max, prompt)
     cap = B.make_capture(rt, plan)
-    runner = B.build(rt, bufs, cap, meta, d, s_max, d.L, True)
+    runner = B.build(rt, bufs, cap, meta, d, s_max, d.L, True, n_splits=args.n_splits, fp8_experts=args.fp8_experts)
     log(f"plan: {len(runner.stages)} stages/iteration, {plan.n_splits} splits of {plan.split}, s_max {s_max}")
     t0 = time.time()
     prefill_warm_s = None
@@ -187,7 +207,7 @@ def main():
     per_launch = [1e3 * rt.marks_ms(i, i + 1) for i in range(K)]
     us_tok = 1e3 * rt.marks_ms(0, K) / K
     ids = runner.host["tokens"].download()[ctx:ctx + K].tolist()
-    mean_bytes = sum(P.bytes_per_token(d, ctx + i) for i in range(K)) / K
+    mean_bytes = sum(P.bytes_per_token(d, ctx + i, fp8_experts=args.fp8_experts) for i in range(K)) / K
     achieved = mean_bytes / (us_tok * 1e-6) / 1e9
     log(f"decode: {us_tok:.1f} us/token (events), wall {wall_ms / K * 1e3:.1f} us/token, per-launch median "
         f"{statistics.median(per_launch):.1f} min {min(per_launch):.1f} max {max(per_launch):.1f} us; "
@@ -196,12 +216,16 @@ def main():
     out = {
         "metric": METRIC, "value": round(us_tok, 2), "unit": "µs/token", "n_gpus": 1, "steps": K, "warmup": Wm,
         "ms_per_step": round(us_tok / 1e3, 5), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
-        "dtype": "bf16", "data": "synthetic: seeded N(0,0.02) bf16 weights, seeded uniform 1024-token prompt",
+        "dtype": "fp8-e4m3 expert weights x bf16" if args.fp8_experts else "bf16",
+        "data": "synthetic: seeded N(0,0.02) bf16 weights" + (" (experts quantized to FP8, per-row scales)"
+                                                              if args.fp8_experts else "")
+                + ", seeded uniform 1024-token prompt",
         "config": {"workload": "BASELINE configs[3]: DeepSeek-V2-Lite 27 layers, 1024-token prompt (prefill untimed), "
                                "greedy decode at batch 1", "layers": d.L, "batch": 1, "ctx": ctx, "decode_tokens": K,
-                   "splits": plan.n_splits, "seed": args.seed},
+                   "splits": plan.n_splits, "seed": args.seed, "fp8_experts": args.fp8_experts},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic_bytes(ctx),
+                     "frac": round(achieved / HBM_PEAK_GBPS, 4),
+                     "traffic": None if args.fp8_experts else traffic_bytes(ctx),
                      "bytes_per_token": int(mean_bytes), "kernel": "fx_persistent"},
         "launch_us_median": round(statistics.median(per_launch), 2), "prefill": args.prefill,
         "prefill_s": round(prefill_s, 3), "prefill_warm_s": None if prefill_warm_s is None else round(prefill_warm_s, 3),

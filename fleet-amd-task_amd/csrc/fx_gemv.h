@@ -13,8 +13,24 @@
 
 template <int R, int NJ>
 struct Tile {
+  static constexpr int kRows = R;
   u32x4 w[R][NJ];
   int row[R];
+};
+
+// FP8 weights (OCP e4m3fn codes, one f32 scale per row): a row of K codes, then the output is
+// scale[row] * dot_lanes16(codes, x): chunk c of 16 contiguous codes (16 bytes) -> lane c % 64,
+// one fma per element in order, the xor butterfly, then one multiply by the row's scale.
+struct Fp8W {
+  const uint8_t* q;   // codes [rows][K]
+  const float* s;     // scale [rows]
+};
+template <int R, int NJ>
+struct TileQ {
+  static constexpr int kRows = R;
+  u32x4 w[R][NJ];
+  int row[R];
+  float sc[R];
 };
 
 template <int R, int NJ, class RowFn>
@@ -61,9 +77,74 @@ __device__ __forceinline__ void tile_dot(const Tile<R, NJ>& t, const float* xs, 
   for (int i = 0; i < R; ++i) acc[i] = butterfly(acc[i], nl);
 }
 
-// Issue the loads of this wave's first group (group index = wave id) into t0.
 template <int R, int NJ, class RowFn>
-__device__ __forceinline__ void gemv_prime(Tile<R, NJ>& t0, const uint16_t* W, int K, int ngroups, RowFn& rowof) {
+__device__ __forceinline__ void tile_load(TileQ<R, NJ>& t, const Fp8W& W, int K, int g, RowFn& rowof) {
+  const int lane = lane_id();
+  const int nchunk = K >> 4;
+  int first = -1;
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    t.row[i] = rowof(g, i);
+    if (first < 0 && t.row[i] >= 0) first = t.row[i];
+  }
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const int c = lane + 64 * j;
+    const int cc = c < nchunk ? c : nchunk - 1;
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+      const int r = t.row[i] >= 0 ? t.row[i] : first;
+      t.w[i][j] = ldw16(W.q + (size_t)r * K + (size_t)cc * 16);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < R; ++i) t.sc[i] = W.s[t.row[i] >= 0 ? t.row[i] : first];
+}
+
+// the 16 codes of a chunk as f32 (the hardware's OCP e4m3fn conversion, byte k = element k)
+__device__ __forceinline__ void unpack16_fp8(u32x4 v, float* d) {
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w[k], false);
+    const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)w[k], true);
+    d[4 * k + 0] = lo[0];
+    d[4 * k + 1] = lo[1];
+    d[4 * k + 2] = hi[0];
+    d[4 * k + 3] = hi[1];
+  }
+}
+
+template <int R, int NJ>
+__device__ __forceinline__ void tile_dot(const TileQ<R, NJ>& t, const float* xs, int K, float* acc) {
+  const int lane = lane_id();
+  const int nchunk = K >> 4;
+#pragma unroll
+  for (int i = 0; i < R; ++i) acc[i] = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const int c = lane + 64 * j;
+    if (c < nchunk) {
+      const float4* xp = (const float4*)(xs + c * 16);
+      const float4 a = xp[0], b = xp[1], e = xp[2], f = xp[3];
+      const float xv[16] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w, e.x, e.y, e.z, e.w, f.x, f.y, f.z, f.w};
+#pragma unroll
+      for (int i = 0; i < R; ++i) {
+        float wv[16];
+        unpack16_fp8(t.w[i][j], wv);
+#pragma unroll
+        for (int k = 0; k < 16; ++k) acc[i] = __builtin_fmaf(wv[k], xv[k], acc[i]);
+      }
+    }
+  }
+  const int nl = lanes_for(nchunk);
+#pragma unroll
+  for (int i = 0; i < R; ++i) acc[i] = butterfly(acc[i], nl) * t.sc[i];
+}
+
+// Issue the loads of this wave's first group (group index = wave id) into t0.
+template <class TileT, class WT, class RowFn>
+__device__ __forceinline__ void gemv_prime(TileT& t0, const WT& W, int K, int ngroups, RowFn& rowof) {
   if (wave_id() < ngroups) tile_load(t0, W, K, wave_id(), rowof);
 }
 
@@ -72,15 +153,15 @@ __device__ __forceinline__ void gemv_prime(Tile<R, NJ>& t0, const uint16_t* W, i
 #ifndef FX_PIPE_DEPTH
 #define FX_PIPE_DEPTH 2
 #endif
-template <int R, int NJ, class RowFn, class XsFn, class EmitFn>
-__device__ __forceinline__ void gemv_pipe_x(Tile<R, NJ>& t0, const uint16_t* W, int K, XsFn xsof, int ngroups,
-                                            RowFn& rowof, EmitFn emit) {
-  Tile<R, NJ> t1;
-  float acc[R];
+template <class TileT, class WT, class RowFn, class XsFn, class EmitFn>
+__device__ __forceinline__ void gemv_pipe_x(TileT& t0, const WT& W, int K, XsFn xsof, int ngroups, RowFn& rowof,
+                                            EmitFn emit) {
+  TileT t1;
+  float acc[TileT::kRows];
   int g = wave_id();
 #if FX_PIPE_DEPTH == 3
   // three tiles in rotation: while one is reduced, the next two are in flight
-  Tile<R, NJ> t2;
+  TileT t2;
   if (g + FX_WAVES < ngroups) tile_load(t1, W, K, g + FX_WAVES, rowof);
   while (g < ngroups) {
     if (g + 2 * FX_WAVES < ngroups) tile_load(t2, W, K, g + 2 * FX_WAVES, rowof);
@@ -114,9 +195,9 @@ __device__ __forceinline__ void gemv_pipe_x(Tile<R, NJ>& t0, const uint16_t* W, 
 #endif
 }
 // the same walk with one input row for every group
-template <int R, int NJ, class RowFn, class EmitFn>
-__device__ __forceinline__ void gemv_pipe(Tile<R, NJ>& t0, const uint16_t* W, int K, const float* xs, int ngroups,
-                                          RowFn& rowof, EmitFn emit) {
+template <class TileT, class WT, class RowFn, class EmitFn>
+__device__ __forceinline__ void gemv_pipe(TileT& t0, const WT& W, int K, const float* xs, int ngroups, RowFn& rowof,
+                                          EmitFn emit) {
   gemv_pipe_x(t0, W, K, [=](int) { return xs; }, ngroups, rowof, emit);
 }
 

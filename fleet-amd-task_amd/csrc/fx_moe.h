@@ -82,7 +82,8 @@ __device__ __forceinline__ void op_moe_router(const fx_stage& s, FxEnv& env) {
 // stream while the router logits are still on their way. With FX_F_ROUTER the stage also computes the router (row e on worker e, W_gate in `res`) and
 // reads the logits back from its own packets. act8[slot][i] = bf16(silu(bf16(W13[e][i] h)) *
 // bf16(W13[e][I + i] h)).
-__device__ __forceinline__ void op_moe_w13(const fx_stage& s, FxEnv& env) {
+template <class TileT, class WT>
+__device__ __forceinline__ void op_moe_w13_t(const fx_stage& s, FxEnv& env, const WT& W) {
   float* xs = (float*)(env.lds + LDS_XS);
   float* red = (float*)(env.lds + LDS_RED);
   int* ids = (int*)(env.lds + LDS_MISC + 128);
@@ -100,7 +101,6 @@ __device__ __forceinline__ void op_moe_w13(const fx_stage& s, FxEnv& env) {
   range_split(nsh * PG, env.nworkers, env.worker, a0, a1);
   range_split(topk * PG, env.nworkers, env.worker, b0, b1);
   const int nA = a1 - a0, nB = b1 - b0;
-  const uint16_t* W = (const uint16_t*)s.w;
   const size_t ex = (size_t)2 * I;   // rows per expert
   auto rowA = [&](int g, int i) {
     const int a = a0 + g;
@@ -114,7 +114,7 @@ __device__ __forceinline__ void op_moe_w13(const fx_stage& s, FxEnv& env) {
     const int p = 2 * (r % PG) + (i >> 1);
     return (int)(e * ex + ((i & 1) ? I + p : p));
   };
-  Tile<4, 4> t0;
+  TileT t0;
   gemv_prime(t0, W, K, nA, rowA);
   const bool rrow = router && env.worker < E;
   const uint16_t* Wg = (const uint16_t*)s.res;
@@ -206,12 +206,26 @@ __device__ __forceinline__ void op_moe_w13(const fx_stage& s, FxEnv& env) {
   prof_mark(env, 2);
 }
 
+// bf16 weights, or FP8 (kFp8, stages flagged FX_F_FP8: the codes [E + n_forced][2 I][K], then their
+// per-row f32 scales)
+template <bool kFp8>
+__device__ __forceinline__ void op_moe_w13(const fx_stage& s, FxEnv& env) {
+  if constexpr (kFp8) {
+    const size_t rows = (size_t)(s.aux_i0 + s.n_forced) * 2 * s.n_rows;
+    const Fp8W W{(const uint8_t*)s.w, (const float*)((const uint8_t*)s.w + rows * (size_t)s.k)};
+    op_moe_w13_t<TileQ<4, 2>>(s, env, W);
+  } else {
+    op_moe_w13_t<Tile<4, 4>>(s, env, (const uint16_t*)s.w);
+  }
+}
+
 // FX_OP_MOE_W2 with the combine: worker w owns output rows [r0, r0 + 8) of every slot; group g is
 // 4 rows of one slot. The shared slots' activations (finished first by the gate|up stage) are
 // awaited and consumed first, then the routed ones; x_new[n] = bf16(x[n] + sum_s out8[s][n] * w_s),
 // multiply then add, in slot order (harness/numpy_ref.py:316-321).
 #define W2_ROWS 8
-__device__ __forceinline__ void op_moe_w2(const fx_stage& s, FxEnv& env) {
+template <class TileT, class WT>
+__device__ __forceinline__ void op_moe_w2_t(const fx_stage& s, FxEnv& env, const WT& W) {
   float* xs = (float*)(env.lds + LDS_XS);        // act8 [8][I]
   float* red = (float*)(env.lds + LDS_RED);
   int* ids = (int*)(env.lds + LDS_MISC + 128);
@@ -227,10 +241,9 @@ __device__ __forceinline__ void op_moe_w2(const fx_stage& s, FxEnv& env) {
   const int nrow = (c1 - c0) * W2_ROWS;          // 8 (H = 2048, 256 workers)
   const int quads = nrow >> 2;
   const int nA = nsh * quads, nB = topk * quads;
-  const uint16_t* W = (const uint16_t*)s.w;
   auto rowA = [&](int g, int i) { return (E + g / quads) * H + r0 + (g % quads) * 4 + i; };
   auto rowB = [&](int g, int i) { return ids[g / quads] * H + r0 + (g % quads) * 4 + i; };
-  Tile<4, 3> t0;
+  TileT t0;
   gemv_prime(t0, W, I, nA, rowA);
   // the usual split (2 quads per worker: one shared and three routed groups per wave): the routed
   // tiles of the wave are requested as soon as the routing is known (the third once the shared
@@ -245,7 +258,7 @@ __device__ __forceinline__ void op_moe_w2(const fx_stage& s, FxEnv& env) {
     poll_logits_wave(lg, (const void*)s.aux[0], E, tag_in(s, env, 1), env.err);
     route_slots_wave(lg, s, ids, wts, nullptr);
   }
-  Tile<4, 3> tr0, tr1;
+  TileT tr0, tr1;
   if (whole) {
     if (!routed_here) __syncthreads();   // ids
     const int w = wave_id();
@@ -320,6 +333,19 @@ __device__ __forceinline__ void op_moe_w2(const fx_stage& s, FxEnv& env) {
     pk_put((void*)s.out, (uint32_t)((r0 >> 1) + threadIdx.x), pack2(red[2 * threadIdx.x], red[2 * threadIdx.x + 1]),
            tag_out(env));
   prof_mark(env, 2);
+}
+
+// bf16 weights, or FP8 (kFp8, stages flagged FX_F_FP8: the codes [E + n_forced][H][I], then their
+// per-row f32 scales)
+template <bool kFp8>
+__device__ __forceinline__ void op_moe_w2(const fx_stage& s, FxEnv& env) {
+  if constexpr (kFp8) {
+    const size_t rows = (size_t)(s.aux_i0 + s.n_forced) * s.n_rows;
+    const Fp8W W{(const uint8_t*)s.w, (const float*)((const uint8_t*)s.w + rows * (size_t)s.k)};
+    op_moe_w2_t<TileQ<4, 2>>(s, env, W);
+  } else {
+    op_moe_w2_t<Tile<4, 3>>(s, env, (const uint16_t*)s.w);
+  }
 }
 
 // FX_OP_ARGMAX: tokens[step + 1] (the reduce of argmax_partial; fleet/graph_plan.py:598-602)

@@ -8,6 +8,9 @@
 #include "fx_mla.h"
 #include "fx_moe.h"
 
+// kFp8: the kernel variant whose expert stages read FP8 weights (a plan's expert stages are all
+// bf16 or all FP8; the launch picks the variant, so each kernel holds one expert path)
+template <bool kFp8 = false>
 __device__ __forceinline__ void run_stage(const fx_stage& s, FxEnv& env) {
   switch (s.op) {
     case FX_OP_GEMV: op_gemv(s, env); break;
@@ -15,8 +18,8 @@ __device__ __forceinline__ void run_stage(const fx_stage& s, FxEnv& env) {
     case FX_OP_MLA_ATTEND: op_mla_attend(s, env); break;
     case FX_OP_MLA_MERGE_UV: op_mla_merge_uv(s, env); break;
     case FX_OP_MOE_ROUTER: op_moe_router(s, env); break;
-    case FX_OP_MOE_W13: op_moe_w13(s, env); break;
-    case FX_OP_MOE_W2: op_moe_w2(s, env); break;
+    case FX_OP_MOE_W13: op_moe_w13<kFp8>(s, env); break;
+    case FX_OP_MOE_W2: op_moe_w2<kFp8>(s, env); break;
     case FX_OP_DENSE_GU: op_dense_gu(s, env); break;
     case FX_OP_ARGMAX: op_argmax(s, env); break;
     default: break;

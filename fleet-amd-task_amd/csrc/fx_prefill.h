@@ -175,3 +175,51 @@ __global__ void __launch_bounds__(PF_THREADS) pf_combine_kernel(const uint16_t* 
     x_res[m * H + c] = (uint16_t)f2bf(acc);
   }
 }
+
+// OCP e4m3fn code of a finite f32 (round to nearest even, saturated at +-448; -0 keeps its sign)
+__device__ __forceinline__ uint32_t f32_to_e4m3(float v) {
+  const uint32_t u = __float_as_uint(v);
+  const uint32_t sign = (u >> 24) & 0x80u;
+  const float a = fabsf(v);
+  uint32_t code;
+  if (!(a < 448.0f)) {
+    code = 0x7Eu;
+  } else if (a < 0.015625f) {                       // below the smallest normal 2^-6: units of 2^-9
+    code = (uint32_t)__builtin_rintf(a * 512.0f);  // 0 .. 8 (8 is the smallest normal, code 0x08)
+  } else {
+    const uint32_t ua = __float_as_uint(a);
+    const int e = (int)(ua >> 23) - 127;            // -6 .. 8
+    const uint32_t m = ua & 0x7FFFFFu;
+    uint32_t q = (m + 0x7FFFFu + ((m >> 20) & 1u)) >> 20;   // 3 mantissa bits, RNE (may carry to 8)
+    uint32_t ex = (uint32_t)(e + 7);
+    if (q == 8u) { q = 0u; ex += 1u; }
+    code = (ex << 3) | q;
+    if (code > 0x7Eu) code = 0x7Eu;
+  }
+  return sign | code;
+}
+
+__global__ void __launch_bounds__(PF_THREADS) fx_quant_fp8_kernel(const uint16_t* src, uint8_t* q, float* s, int K) {
+  __shared__ float red[PF_THREADS / 64];
+  const size_t r = blockIdx.x;
+  const uint16_t* row = src + r * K;
+  float amax = 0.0f;
+  for (int j = threadIdx.x; j < K; j += PF_THREADS) amax = fmaxf(amax, fabsf(bf2f(row[j])));
+  amax = pf_block_max(amax, red);
+  const float scale = amax > 0.0f ? amax / 448.0f : 1.0f;
+  for (int j = threadIdx.x; j < K; j += PF_THREADS) q[r * K + j] = (uint8_t)f32_to_e4m3(bf2f(row[j]) / scale);
+  if (threadIdx.x == 0) s[r] = scale;
+}
+
+// dst[r][j] = bf16(e4m3(codes[r][j]) * scale[r]): FP8 rows back to bf16 (the batched prefill's GEMMs)
+__global__ void __launch_bounds__(PF_THREADS) fx_dequant_fp8_kernel(const uint8_t* q, const float* s, uint16_t* dst,
+                                                                   int K) {
+  const size_t r = blockIdx.x;
+  const float sc = s[r];
+  for (int j = threadIdx.x * 16; j < K; j += PF_THREADS * 16) {
+    float v[16];
+    unpack16_fp8(*(const u32x4*)(q + r * K + j), v);
+#pragma unroll
+    for (int k = 0; k < 16; ++k) dst[r * K + j + k] = (uint16_t)f2bf(v[k] * sc);
+  }
+}

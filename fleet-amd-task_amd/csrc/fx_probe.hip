@@ -247,6 +247,19 @@ __global__ void fxp_pingpong_kernel(uint32_t* flag, int a, int b, uint32_t round
 
 // ---- lane exchange check: out[lane * 6 + k] = the value xor_lane<2^k> returns on `lane` when every
 // lane holds its own index (must be lane ^ 2^k)
+// ---- FP8 decode: the 256 codes through the hardware's packed FP8 -> f32 conversion (lane l: codes
+// 4l .. 4l + 3 as one 32-bit word; word_sel false takes bytes 0, 1, true bytes 2, 3)
+__global__ void fxp_fp8_kernel(float* out) {
+  const int l = threadIdx.x & 63;
+  const int src = (4 * l) | ((4 * l + 1) << 8) | ((4 * l + 2) << 16) | ((4 * l + 3) << 24);
+  const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8(src, false);
+  const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8(src, true);
+  out[4 * l + 0] = lo[0];
+  out[4 * l + 1] = lo[1];
+  out[4 * l + 2] = hi[0];
+  out[4 * l + 3] = hi[1];
+}
+
 __global__ void fxp_lanes_kernel(float* out) {
   const float v = (float)(threadIdx.x & 63);
   const int l = threadIdx.x & 63;
@@ -404,6 +417,17 @@ int fxp_clock(int iters, const void* load, uint64_t load_bytes, uint64_t* out_ho
   e = hipMemcpy(out_host, out, 24, hipMemcpyDeviceToHost);
   (void)hipFree(done);
   (void)hipFree(out);
+  return e;
+}
+
+int fxp_fp8(float* out_host) {
+  float* d = nullptr;
+  hipError_t e;
+  if ((e = hipMalloc(&d, 256 * 4)) != hipSuccess) return e;
+  hipLaunchKernelGGL(fxp_fp8_kernel, dim3(1), dim3(64), 0, 0, d);
+  if ((e = hipDeviceSynchronize()) != hipSuccess) return e;
+  e = hipMemcpy(out_host, d, 256 * 4, hipMemcpyDeviceToHost);
+  (void)hipFree(d);
   return e;
 }
 

@@ -59,6 +59,7 @@ __device__ __forceinline__ void env_init(FxEnv& env, char* lds, int64_t* tokens,
   env.route_tag = 0;
 }
 
+template <bool kFp8>
 __device__ __forceinline__ void persistent_body(const FxRunArgs& a) {
   extern __shared__ __attribute__((aligned(16))) char lds[];
   const int b = blockIdx.x;
@@ -87,7 +88,7 @@ __device__ __forceinline__ void persistent_body(const FxRunArgs& a) {
       env.sidx = s;
       env.pst = prof ? a.prof + ((size_t)s * FX_BLOCKS + b) * FX_PROF_SLOTS : nullptr;
       prof_mark(env, 0);
-      run_stage(*sst, env);
+      run_stage<kFp8>(*sst, env);
       if (prof) {
         __syncthreads();
         prof_mark(env, 3);
@@ -101,7 +102,7 @@ __device__ __forceinline__ void persistent_body(const FxRunArgs& a) {
   for (int s = 0; s < a.n_epi; ++s) {
     __syncthreads();
     env.sidx = a.n_stages + s;
-    run_stage(table[a.n_stages + s], env);
+    run_stage<kFp8>(table[a.n_stages + s], env);
   }
   if (b == 0 && threadIdx.x == 0 && a.timing) a.timing[a.iters] = __builtin_amdgcn_s_memrealtime();
 }
@@ -109,8 +110,11 @@ __device__ __forceinline__ void persistent_body(const FxRunArgs& a) {
 // The decode launch (iterations that end in the LM head + argmax) and the prefill launch (prompt
 // positions only: the head stages are skipped) run the same body; they are two symbols so that a
 // kernel trace attributes prefill and decode time separately.
-__global__ void __launch_bounds__(FX_THREADS) fx_persistent(FxRunArgs a) { persistent_body(a); }
-__global__ void __launch_bounds__(FX_THREADS) fx_prefill(FxRunArgs a) { persistent_body(a); }
+__global__ void __launch_bounds__(FX_THREADS) fx_persistent(FxRunArgs a) { persistent_body<false>(a); }
+__global__ void __launch_bounds__(FX_THREADS) fx_prefill(FxRunArgs a) { persistent_body<false>(a); }
+// the same with FP8 expert weights (plans whose expert stages carry FX_F_FP8)
+__global__ void __launch_bounds__(FX_THREADS) fx_persistent_fp8(FxRunArgs a) { persistent_body<true>(a); }
+__global__ void __launch_bounds__(FX_THREADS) fx_prefill_fp8(FxRunArgs a) { persistent_body<true>(a); }
 
 // one stage as a standalone launch (kernel suite): same work split; packet inputs carry
 // tbase + src[k] + 1, outputs tbase + sidx + 1
@@ -258,6 +262,7 @@ struct fx_ctx {
   size_t prof_words = 0;
   int prof_iter = -1;
   rocblas_handle blas = nullptr;   // the prefill's GEMMs (created on first use)
+  bool fp8 = false;                // the loaded plan's expert stages read FP8 weights
 };
 
 static int fail(fx_ctx* c, int code, const std::string& msg) {
@@ -295,6 +300,8 @@ int fx_create(int device, fx_ctx** out) {
   *out = c;
   HIPCHK(c, hipFuncSetAttribute((const void*)fx_persistent, hipFuncAttributeMaxDynamicSharedMemorySize, FX_LDS_TOTAL));
   HIPCHK(c, hipFuncSetAttribute((const void*)fx_prefill, hipFuncAttributeMaxDynamicSharedMemorySize, FX_LDS_TOTAL));
+  HIPCHK(c, hipFuncSetAttribute((const void*)fx_persistent_fp8, hipFuncAttributeMaxDynamicSharedMemorySize, FX_LDS_TOTAL));
+  HIPCHK(c, hipFuncSetAttribute((const void*)fx_prefill_fp8, hipFuncAttributeMaxDynamicSharedMemorySize, FX_LDS_TOTAL));
   HIPCHK(c, hipFuncSetAttribute((const void*)fx_stage_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, FX_LDS_BYTES));
   HIPCHK(c, hipFuncSetAttribute((const void*)fx_xcc_map, hipFuncAttributeMaxDynamicSharedMemorySize, FX_LDS_BYTES));
   HIPCHK(c, hipMalloc(&c->err_flag, FX_ERR_WORDS * 4));
@@ -377,6 +384,10 @@ static int check_stage(fx_ctx* c, const fx_stage& s, int idx, int n_total) {
   auto bad = [&](const std::string& m) { return fail(c, FX_E_ARG, "stage " + std::to_string(idx) + ": " + m); };
   for (int k = 0; k < 4; ++k)
     if (s.src[k] < -n_total || s.src[k] >= n_total) return bad("packet source out of range");
+  if (s.flags & FX_F_FP8) {
+    if (s.op != FX_OP_MOE_W13 && s.op != FX_OP_MOE_W2) return bad("FP8 weights are read by the expert stages only");
+    if (s.k % 16 || (s.k / 16 + 63) / 64 > 2) return bad("FP8 K must be a multiple of 16, at most 2048");
+  }
   switch (s.op) {
     case FX_OP_GEMV: {
       if (!s.w || !s.out || s.n_rows <= 0 || s.k <= 0 || s.k % 8) return bad("gemv shape/pointers");
@@ -457,6 +468,14 @@ int fx_load_plan(fx_ctx* c, const fx_stage* st, int32_t n, const fx_stage* epi, 
     int r = check_stage(c, epi[i], n + i, n);
     if (r) return r;
   }
+  // a plan's expert stages are all bf16 or all FP8: the launch picks the kernel variant
+  int n_fp8 = 0, n_exp = 0;
+  for (int i = 0; i < n; ++i)
+    if (st[i].op == FX_OP_MOE_W13 || st[i].op == FX_OP_MOE_W2) {
+      ++n_exp;
+      n_fp8 += (st[i].flags & FX_F_FP8) != 0;
+    }
+  if (n_fp8 && n_fp8 != n_exp) return fail(c, FX_E_ARG, "a plan's expert stages must be all bf16 or all FP8");
   if (c->d_stages) { HIPCHK(c, hipFree(c->d_stages)); c->d_stages = nullptr; }
   if (c->d_epi) { HIPCHK(c, hipFree(c->d_epi)); c->d_epi = nullptr; }
   HIPCHK(c, hipMalloc(&c->d_stages, sizeof(fx_stage) * n));
@@ -467,6 +486,7 @@ int fx_load_plan(fx_ctx* c, const fx_stage* st, int32_t n, const fx_stage* epi, 
   }
   c->n_stages = n;
   c->n_epi = n_epi;
+  c->fp8 = n_fp8 > 0;
   c->h_stages.assign(st, st + n);
   c->h_epi.assign(epi ? epi : st, epi ? epi + n_epi : st);
   return FX_OK;
@@ -512,7 +532,8 @@ int fx_launch(fx_ctx* c, int32_t iters, int32_t step0, int32_t n_prompt, int64_t
   void* args[] = {&a};
   // every iteration skips the head (all positions inside the prompt): the prefill symbol
   const bool prefill = (int64_t)step0 + iters < (int64_t)n_prompt;
-  const void* fn = prefill ? (const void*)fx_prefill : (const void*)fx_persistent;
+  const void* fn = c->fp8 ? (prefill ? (const void*)fx_prefill_fp8 : (const void*)fx_persistent_fp8)
+                          : (prefill ? (const void*)fx_prefill : (const void*)fx_persistent);
   HIPCHK(c, hipEventRecord(c->ev0, s));
   HIPCHK(c, hipLaunchCooperativeKernel(fn, dim3(FX_BLOCKS), dim3(FX_THREADS), args, FX_LDS_TOTAL, s));
   HIPCHK(c, hipEventRecord(c->ev1, s));
@@ -585,6 +606,7 @@ int fx_run_stage(fx_ctx* c, const fx_stage* st, int32_t step, uint32_t tbase, in
   if (!c || !st) return FX_E_ARG;
   int r = check_stage(c, *st, 0, 1 << 20);
   if (r) return r;
+  if (st->flags & FX_F_FP8) return fail(c, FX_E_ARG, "FP8 expert stages run in the persistent kernel only");
   hipStream_t s = (hipStream_t)stream;
   // the embed prologue reads tokens[step]; the argmax reduce always stores tokens[step + 1]
   const int n_prompt = st->op == FX_OP_ARGMAX ? 0 : (1 << 30);
@@ -606,6 +628,7 @@ int fx_time_stages(fx_ctx* c, const fx_stage* st, int32_t n, int32_t reps, int32
   for (int i = 0; i < n; ++i) {
     int r = check_stage(c, st[i], i, 1 << 20);
     if (r) return r;
+    if (st[i].flags & FX_F_FP8) return fail(c, FX_E_ARG, "FP8 expert stages run in the persistent kernel only");
   }
   hipStream_t s = (hipStream_t)stream;
   int n_prompt = 1 << 30;
@@ -797,6 +820,30 @@ int fx_pf_combine(fx_ctx* c, const void* x_mid, const void* og, const void* inv,
   PF_CHECK(c, x_mid && og && inv && w && x_res && M > 0 && H > 0 && slots > 0, "fx_pf_combine: arguments");
   hipLaunchKernelGGL(pf_combine_kernel, dim3(M), dim3(PF_THREADS), 0, (hipStream_t)stream, (const uint16_t*)x_mid,
                      (const uint16_t*)og, (const int32_t*)inv, (const float*)w, (uint16_t*)x_res, H, slots);
+  HIPCHK(c, hipGetLastError());
+  return FX_OK;
+}
+
+// FP8 rows from bf16 rows (weight-only quantization): scale = max|w| / 448 (1 for an all-zero row),
+// codes = e4m3fn(w / scale) rounded to nearest even, saturated at 448; dst holds the rows' codes,
+// then their f32 scales.
+int fx_quantize_fp8(fx_ctx* c, const void* src, void* dst, int64_t rows, int32_t K, void* stream) {
+  if (!c) return FX_E_ARG;
+  PF_CHECK(c, src && dst && rows > 0 && rows <= 0x7fffffff && K > 0 && K % 16 == 0 && al16(src) && al16(dst),
+           "fx_quantize_fp8: arguments");
+  hipLaunchKernelGGL(fx_quant_fp8_kernel, dim3((unsigned)rows), dim3(PF_THREADS), 0, (hipStream_t)stream,
+                     (const uint16_t*)src, (uint8_t*)dst, (float*)((uint8_t*)dst + rows * K), K);
+  HIPCHK(c, hipGetLastError());
+  return FX_OK;
+}
+
+// bf16 rows from FP8 rows (codes then scales, as fx_quantize_fp8 writes them)
+int fx_dequantize_fp8(fx_ctx* c, const void* src, void* dst, int64_t rows, int32_t K, void* stream) {
+  if (!c) return FX_E_ARG;
+  PF_CHECK(c, src && dst && rows > 0 && rows <= 0x7fffffff && K > 0 && K % 16 == 0 && al16(src) && al16(dst),
+           "fx_dequantize_fp8: arguments");
+  hipLaunchKernelGGL(fx_dequant_fp8_kernel, dim3((unsigned)rows), dim3(PF_THREADS), 0, (hipStream_t)stream,
+                     (const uint8_t*)src, (const float*)((const uint8_t*)src + rows * K), (uint16_t*)dst, K);
   HIPCHK(c, hipGetLastError());
   return FX_OK;
 }

@@ -148,6 +148,8 @@ def compile_stages(plan, host):
                              4: B(a["logits"]), 5: rl.ptr, 6: B(a["h"]), 7: B(a["sel"])}, **common)
             ins = [(1, a["input"])]
             lab = c.label
+            if plan.fp8_experts:
+                st.flags |= R.FX_F_FP8
             if pend_router is not None:
                 assert pend_router.args["w_norm"] == a["w_norm"] and pend_router.args["logits_x"] == a["logits_x"]
                 st.flags |= R.FX_F_ROUTER
@@ -164,6 +166,8 @@ def compile_stages(plan, host):
                         scaling=G.ROUTED_SCALING, aux_i0=d.E, x=B(a["input"]), w=B(a["weight"]),
                         res=B(comb.args["residual"]), out=B(comb.args["output"]),
                         aux={0: B(a["logits_x"]), 1: B(a["output"])}, **common)
+            if plan.fp8_experts:
+                st.flags |= R.FX_F_FP8
             ins = [(0, a["input"]), (1, a["logits_x"]), (2, comb.args["residual"])]
         else:
             raise ValueError(f"unknown plan method {m}")
@@ -318,7 +322,7 @@ def build(rt, packed, capture, meta, dims: Dims = REAL_DIMS, s_max=1056, layers=
 
 def plan_json(plan):
     return {"dims": plan.dims.__dict__, "s_max": plan.s_max, "layers": plan.layers, "head": plan.head,
-            "split": plan.split, "n_splits": plan.n_splits,
+            "split": plan.split, "n_splits": plan.n_splits, "fp8_experts": plan.fp8_experts,
             "calls": [{"method": c.method, "label": c.label, "tasks": c.tasks,
                        "args": {k: v for k, v in c.args.items() if isinstance(v, (str, int, float, bool)) or v is None}}
                       for c in plan.calls]}

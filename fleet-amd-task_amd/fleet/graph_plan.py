@@ -14,7 +14,7 @@ between two packet vectors, x_res (layer input) and x_mid (after attention).
 import struct
 from dataclasses import dataclass, field
 
-from fleet.pack_weights import Dims, REAL_DIMS, XCDS
+from fleet.pack_weights import Dims, REAL_DIMS, XCDS, fp8_nbytes
 
 SPLIT = 32                 # positions per attention split (the reference's D11); tiles of 32
 N_FORCED = 2
@@ -83,6 +83,7 @@ class Plan:
     n_splits: int
     tensors: dict = field(default_factory=dict)
     calls: list = field(default_factory=list)
+    fp8_experts: bool = False   # W13 / W2 are FP8 (codes + per-row scales, pack_weights.quantize_experts)
 
     def t(self, name, shape, dtype="bf16", kind="new", source=""):
         assert name not in self.tensors, name
@@ -152,7 +153,7 @@ def default_splits(s_max):
 
 def build_plan(dims: Dims = REAL_DIMS, s_max: int = 1056, layers: int = 27, head: bool = True, split: int = None,
                n_splits: int = None, iters_cap: int = 32, softmax_scale: float = SOFTMAX_SCALE,
-               eps: float = RMS_EPS) -> Plan:
+               eps: float = RMS_EPS, fp8_experts: bool = False) -> Plan:
     """split / n_splits: the attention split (positions) or split count; neither: default_splits."""
     d = dims
     assert 1 <= layers <= d.L
@@ -160,6 +161,7 @@ def build_plan(dims: Dims = REAL_DIMS, s_max: int = 1056, layers: int = 27, head
     p = Plan(d, s_max, layers, head, split, n_splits)
     p.scale = softmax_scale
     p.eps = eps
+    p.fp8_experts = fp8_experts
     p.iters_cap = iters_cap
     # ---- meta and shared tensors
     p.t("tokens", (s_max + 1,), "i64", "input", "meta:tokens")
@@ -224,8 +226,12 @@ def build_plan(dims: Dims = REAL_DIMS, s_max: int = 1056, layers: int = 27, head
                  residual="x_mid", output="x_res", norm=False)
         else:
             p.t(f"W_gate_{l}", (d.E, d.H), kind="input", source=f"W_gate_{l}")
-            p.t(f"W13_{l}", (d.E_TOTAL, 2 * d.I_MOE, d.H), kind="input", source=f"W13_{l}")
-            p.t(f"W2_{l}", (d.E_TOTAL, d.H, d.I_MOE), kind="input", source=f"W2_{l}")
+            if fp8_experts:
+                p.t(f"W13_{l}", (fp8_nbytes(d, "W13"),), "u8", kind="input", source=f"W13q_{l}")
+                p.t(f"W2_{l}", (fp8_nbytes(d, "W2"),), "u8", kind="input", source=f"W2q_{l}")
+            else:
+                p.t(f"W13_{l}", (d.E_TOTAL, 2 * d.I_MOE, d.H), kind="input", source=f"W13_{l}")
+                p.t(f"W2_{l}", (d.E_TOTAL, d.H, d.I_MOE), kind="input", source=f"W2_{l}")
             p.op("moe_router_layer", d.E, f"L{l}.router", input="x_mid", w_norm=f"w_norm2_{l}",
                  w_gate=f"W_gate_{l}", logits_x="logits_x")
             p.op("gang_moe_w13_gemv_layer", WORKERS, f"L{l}.w13", input="x_mid", w_norm=f"w_norm2_{l}",

@@ -221,13 +221,17 @@ def packed_bytes(d: Dims = REAL_DIMS):
     return 2 * (2 * d.V * d.H + d.H + d.L * per_layer + dense + (d.L - 1) * moe)
 
 
-def bytes_per_token(d: Dims = REAL_DIMS, ctx: int = 1024, layers: int = None, head: bool = True):
+def bytes_per_token(d: Dims = REAL_DIMS, ctx: int = 1024, layers: int = None, head: bool = True,
+                    fp8_experts: bool = False):
     """Algorithmic HBM bytes of one decode step attending over `ctx` positions (positions 0..ctx-1):
     every weight the step touches once (8 of the 66 experts per MoE layer) plus the latent-cache rows
-    read, plus the embedding row. Activations (KBs) are not counted."""
+    read, plus the embedding row. Activations (KBs) are not counted. fp8_experts: the experts' weights
+    at one byte each plus one f32 scale per row."""
     L = d.L if layers is None else layers
     attn = (d.Q_OUT + d.KVA_OUT) * d.H + d.KVB_OUT * d.D_C + d.H * d.NH * d.D_V + 2 * d.H + d.D_C
     moe = d.E * d.H + d.N_SLOTS * 3 * d.I_MOE * d.H
+    if fp8_experts:   # in bf16 units (the sum is doubled below)
+        moe = d.E * d.H + (d.N_SLOTS * 3 * d.I_MOE * d.H + 4 * d.N_SLOTS * (2 * d.I_MOE + d.H)) // 2
     dense = 3 * d.I_DENSE * d.H
     w = L * attn + (dense if L >= 1 else 0) + max(0, L - 1) * moe + d.H
     if head:
@@ -251,6 +255,39 @@ def fill_seeded(rt, d: Dims = REAL_DIMS, seed: int = 0, layers: int = None, head
                 rt.gen_normal_bf16(buf, s.n, seed, s.stream, s.scale, dst_offset=s.dst_offset, src_offset=s.src_offset,
                                    rows=s.rows, row_len=s.row_len, dst_stride=s.dst_stride, src_stride=s.src_stride)
         bufs[key] = buf
+    rt.synchronize()
+    return bufs
+
+
+# ---- FP8 expert weights ---------------------------------------------------------------------------
+
+def fp8_rows(d: Dims, key: str):
+    """(rows, K) of the FP8 form of a W13 / W2 packed key (rows over all E + N_SHARED experts)."""
+    if key.startswith("W13"):
+        return d.E_TOTAL * 2 * d.I_MOE, d.H
+    return d.E_TOTAL * d.H, d.I_MOE
+
+
+def fp8_nbytes(d: Dims, key: str):
+    """Bytes of an FP8 expert key: the codes [rows][K], then one f32 scale per row."""
+    rows, K = fp8_rows(d, key)
+    return rows * K + 4 * rows
+
+
+def quantize_experts(rt, bufs, d: Dims, layers: int = None, free_bf16: bool = True):
+    """Add W13q_l / W2q_l (FP8 codes + per-row scales, fx_quantize_fp8) for every MoE layer from the
+    bf16 W13_l / W2_l in `bufs` (weight-only, per output row: scale = max|w| / 448); the bf16 expert
+    keys are freed unless free_bf16 is False. Returns bufs."""
+    L = d.L if layers is None else layers
+    for l in range(1, L):
+        for key in (f"W13_{l}", f"W2_{l}"):
+            rows, K = fp8_rows(d, key)
+            q = rt.alloc((fp8_nbytes(d, key),), "u8")
+            rt.check(rt.L.fx_quantize_fp8(rt.h, bufs[key].ptr, q.ptr, rows, K, None), "fx_quantize_fp8")
+            bufs[key.replace("_", "q_", 1)] = q
+            if free_bf16:
+                rt.synchronize()
+                bufs.pop(key).free()
     rt.synchronize()
     return bufs
 

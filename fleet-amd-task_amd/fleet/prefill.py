@@ -21,7 +21,8 @@ kernels, which round at the decode spec's points (numpy_ref.py). Per layer, M = 
            by expert (host), gathered; per expert bf16(h W13[e]^T) -> silu -> bf16(. W2[e]^T);
            x = bf16(x_mid + sum_s out_s w_s) in slot order (fx_pf_combine)
 
-Attention is one softmax over the whole causal row (the decode splits it into 32-position tiles
+With FP8 experts (W13q_l / W2q_l) each layer's experts are expanded back to bf16 (code x row scale,
+fx_dequantize_fp8) for the GEMMs. Attention is one softmax over the whole causal row (the decode splits it into 32-position tiles
 with an online softmax), and the GEMMs reduce in rocBLAS's order, so the cache rows agree with the
 decode path's within bf16 rounding, not bit for bit; a route may differ where two router
 probabilities are within rounding of each other.
@@ -74,6 +75,9 @@ class Prefill:
             self.mid = a((M * S, 2 * d.I_MOE), "bf16")
             self.act8 = a((M * S, d.I_MOE), "bf16")
             self.og = a((M * S, d.H), "bf16")
+            if "W13q_1" in packed:   # FP8 experts: each layer's experts back to bf16 for the GEMMs
+                self.w13 = a((d.E_TOTAL, 2 * d.I_MOE, d.H), "bf16")
+                self.w2 = a((d.E_TOTAL, d.H, d.I_MOE), "bf16")
 
     # ---- thin wrappers (pointers as ints, byte offsets added by the caller) ----------------------
     def gemm(self, ta, tb, M, N, K, A, lda, B, ldb, D, ldd, d_f32=False, beta=0.0, C=None, ldc=0, batch=1,
@@ -162,7 +166,12 @@ class Prefill:
         self.perm.upload(perm)
         self.inv.upload(inv)
         rt.check(L.fx_pf_gather(rt.h, self.h.ptr, self.perm.ptr, self.hg.ptr, M * S, H, None), "fx_pf_gather")
-        W13, W2 = W[f"W13_{l}"], W[f"W2_{l}"]
+        if f"W13q_{l}" in W:
+            for key, dst, rows, K in ((f"W13q_{l}", self.w13, d.E_TOTAL * 2 * I, H), (f"W2q_{l}", self.w2, d.E_TOTAL * H, I)):
+                rt.check(L.fx_dequantize_fp8(rt.h, W[key].ptr, dst.ptr, rows, K, None), "fx_dequantize_fp8")
+            W13, W2 = self.w13, self.w2
+        else:
+            W13, W2 = W[f"W13_{l}"], W[f"W2_{l}"]
         off = 0
         for e in range(d.E_TOTAL):
             n = int(counts[e])

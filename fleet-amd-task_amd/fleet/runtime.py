@@ -22,6 +22,7 @@ FX_OP_MOE_ROUTER, FX_OP_MOE_W13, FX_OP_MOE_W2 = 5, 6, 7
 FX_OP_DENSE_GU, FX_OP_ARGMAX = 9, 10
 FX_IN_VEC, FX_IN_EMBED = 0, 1
 FX_F_NORM, FX_F_RESIDUAL, FX_F_ARGMAX, FX_F_HEAD, FX_F_OUT_LL, FX_F_RES_EMBED, FX_F_ROUTER = 1, 2, 8, 16, 32, 64, 128
+FX_F_FP8 = 256
 FX_MAX_ITERS, FX_MAX_MARKS, FX_PROF_SLOTS = 65536, 256, 8
 FX_ABI_VERSION = 4
 WORKERS = 256          # one worker workgroup per CU
@@ -102,6 +103,8 @@ def lib():
                                           ctypes.POINTER(ctypes.c_float)]),
         "fx_gen_normal_bf16": (ctypes.c_int, [vp, vp, u64, u64, u64, u64, u64, u64, ctypes.c_uint32, ctypes.c_float]),
         "fx_fill_u16": (ctypes.c_int, [vp, vp, u64, ctypes.c_uint16]),
+        "fx_quantize_fp8": (ctypes.c_int, [vp, vp, vp, i64, i32, vp]),
+        "fx_dequantize_fp8": (ctypes.c_int, [vp, vp, vp, i64, i32, vp]),
         "fx_gemm": (ctypes.c_int, [vp, i32, i32, i32, i32, i32, ctypes.c_float, vp, i64, i64, vp, i64, i64,
                                    ctypes.c_float, vp, i64, i64, vp, i64, i64, i32, i32, vp]),
         "fx_pf_embed": (ctypes.c_int, [vp, vp, vp, vp, i32, i32, vp]),
@@ -128,7 +131,7 @@ EXPORTS = ("fx_abi_version", "fx_create", "fx_destroy", "fx_last_error", "fx_dev
            "fx_memcpy_htod", "fx_memcpy_dtoh", "fx_memcpy_dtod", "fx_memset", "fx_synchronize", "fx_load_plan",
            "fx_run", "fx_launch", "fx_finish", "fx_mark", "fx_marks_ms", "fx_last_run_ms", "fx_set_profile",
            "fx_read_profile", "fx_read_timing", "fx_run_stage", "fx_time_stages", "fx_gen_normal_bf16", "fx_fill_u16",
-           "fx_gemm", "fx_pf_embed", "fx_pf_rmsnorm", "fx_pf_prep", "fx_pf_softmax", "fx_pf_attn_out", "fx_pf_silu",
+           "fx_quantize_fp8", "fx_dequantize_fp8", "fx_gemm", "fx_pf_embed", "fx_pf_rmsnorm", "fx_pf_prep", "fx_pf_softmax", "fx_pf_attn_out", "fx_pf_silu",
            "fx_pf_route", "fx_pf_gather", "fx_pf_combine")
 
 

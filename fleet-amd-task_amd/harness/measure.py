@@ -26,10 +26,16 @@ from fleet import pack_weights as P  # noqa: E402
 from fleet import runtime as R  # noqa: E402
 
 
+EXPERT_BYTES = 2   # bytes per expert weight (1 with FP8 experts, plus the per-row scales)
+
+
 def stage_bytes(d, label, ctx):
     """Algorithmic bytes a stage streams (weights it touches + cache rows), for the GB/s column."""
     op = label.split(".", 1)[1].split("+")[0] if "." in label else label
     H = d.H
+    if EXPERT_BYTES == 1 and op in ("w13", "w2"):
+        rows, K = (2 * d.I_MOE, H) if op == "w13" else (H, d.I_MOE)
+        return d.N_SLOTS * rows * (K + 4)
     return {
         "qkva": (d.Q_OUT + d.KVA_OUT) * H * 2, "mla_prep": d.NH * d.D_N * d.D_C * 2,
         "mla_attend": ctx * (d.D_C + d.D_R) * 2, "mla_merge_uv": d.NH * d.D_V * d.D_C * 2,
@@ -86,15 +92,23 @@ def main():
     ap.add_argument("--seed", type=int, default=20261201)
     ap.add_argument("--out", default=None)
     ap.add_argument("--json", default=None)
+    ap.add_argument("--n-splits", type=int, default=None, help="attention splits (default: 32-position splits)")
+    ap.add_argument("--fp8-experts", action="store_true", help="FP8 expert weights (pack_weights.quantize_experts)")
     args = ap.parse_args()
     d = P.REAL_DIMS
     rt = R.Runtime(0)
     ctx = args.ctx
     s_max = ctx + args.iters
     bufs = P.fill_seeded(rt, d, args.seed, args.layers, True)
+    if args.fp8_experts:
+        P.quantize_experts(rt, bufs, d, args.layers)
+        global EXPERT_BYTES
+        EXPERT_BYTES = 1
     prompt = P.prompt_ids(args.seed, ctx, d.V)
-    plan = G.build_plan(d, s_max, args.layers, True)
-    runner = B.build(rt, bufs, B.make_capture(rt, plan), B.make_meta(rt, s_max, prompt), d, s_max, args.layers, True)
+    kw = dict(n_splits=args.n_splits, fp8_experts=args.fp8_experts)
+    plan = G.build_plan(d, s_max, args.layers, True, **kw)
+    runner = B.build(rt, bufs, B.make_capture(rt, plan), B.make_meta(rt, s_max, prompt), d, s_max, args.layers, True,
+                     **kw)
     runner.run(ctx - 1, 0, ctx)
     rows = runner.profile(args.iters, ctx - 1, ctx, args.iter)
     it_us = runner.timing_us()

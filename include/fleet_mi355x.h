@@ -111,6 +111,7 @@ enum fx_op {
 #define FX_F_OUT_LL 32u    /* output as packets */
 #define FX_F_RES_EMBED 64u /* residual = the embedding row of this iteration's token */
 #define FX_F_ROUTER 128u   /* MOE_W13 computes the router itself (W_gate in res) */
+#define FX_F_FP8 256u      /* MOE_W13 / MOE_W2: w is FP8 (OCP e4m3fn codes, then one f32 scale per row) */
 
 /* One entry of the task table: one operator of the plan (fleet/graph_plan.py Call). */
 typedef struct fx_stage {
@@ -221,6 +222,15 @@ int fx_time_stages(fx_ctx* ctx, const fx_stage* stages, int32_t n, int32_t reps,
 int fx_gen_normal_bf16(fx_ctx* ctx, void* dst, uint64_t rows, uint64_t row_len, uint64_t dst_stride,
                        uint64_t src_offset, uint64_t src_stride, uint64_t seed, uint32_t stream, float scale);
 int fx_fill_u16(fx_ctx* ctx, void* dst, uint64_t n, uint16_t value);
+
+/* ---- FP8 expert weights ------------------------------------------------------------------------ */
+/* Weight-only FP8 of `rows` bf16 rows of K (K % 16 == 0): dst = the rows' OCP e4m3fn codes [rows][K]
+ * (w / scale rounded to nearest even, saturated at 448), then their f32 scales [rows] (max|w| / 448,
+ * 1 for an all-zero row). The W13 / W2 stages read it with FX_F_FP8. The reference only projects
+ * this (README.md:130 "FP8 (stretch)", docs/acceleration/04-technique-ledger.md:12, weight-only). */
+int fx_quantize_fp8(fx_ctx* ctx, const void* src, void* dst, int64_t rows, int32_t K, void* stream);
+/* The inverse for the batched prefill's GEMMs: dst[r][j] = bf16(e4m3(codes[r][j]) * scale[r]). */
+int fx_dequantize_fp8(fx_ctx* ctx, const void* src, void* dst, int64_t rows, int32_t K, void* stream);
 
 /* ---- batched prefill (fleet/prefill.py) ------------------------------------------------------- */
 /* The prompt's forward pass over M positions at once, writing the latent-cache rows the decode

@@ -466,6 +466,121 @@ void or_moe_w13_silu(const uint16_t* h, const uint16_t* W13, const int32_t* mask
   free(hf);
 }
 
+/* ---- FP8 expert weights (weight-only OCP e4m3fn, one f32 scale per row) --------------------- */
+/* Decode of the 256 codes: sign, 4 exponent bits (bias 7), 3 mantissa bits; exponent 0 is
+ * subnormal (m * 2^-9); 0x7F / 0xFF are NaN (no infinities). */
+static float e4m3_tab[256];
+static int e4m3_ready = 0;
+static void e4m3_init(void) {
+  if (e4m3_ready) return;
+  for (int c = 0; c < 256; ++c) {
+    int e = (c >> 3) & 15, m = c & 7;
+    float v;
+    if (e == 15 && m == 7) v = NAN;
+    else if (e == 0) v = ldexpf((float)m, -9);
+    else v = ldexpf(1.0f + (float)m / 8.0f, e - 7);
+    e4m3_tab[c] = (c & 0x80) ? -v : v;
+  }
+  e4m3_ready = 1;
+}
+void or_e4m3_decode(float* out) {
+  e4m3_init();
+  memcpy(out, e4m3_tab, sizeof(e4m3_tab));
+}
+
+/* code of a finite f32: round to nearest even, saturated at +-448 */
+static uint8_t e4m3_encode(float v) {
+  uint32_t u;
+  memcpy(&u, &v, 4);
+  uint32_t sign = (u >> 24) & 0x80u;
+  float a = fabsf(v);
+  uint32_t code;
+  if (!(a < 448.0f)) {
+    code = 0x7Eu;
+  } else if (a < 0.015625f) {
+    code = (uint32_t)rintf(a * 512.0f);
+  } else {
+    uint32_t ua;
+    memcpy(&ua, &a, 4);
+    int e = (int)(ua >> 23) - 127;
+    uint32_t m = ua & 0x7FFFFFu;
+    uint32_t q = (m + 0x7FFFFu + ((m >> 20) & 1u)) >> 20;
+    uint32_t ex = (uint32_t)(e + 7);
+    if (q == 8u) { q = 0u; ex += 1u; }
+    code = (ex << 3) | q;
+    if (code > 0x7Eu) code = 0x7Eu;
+  }
+  return (uint8_t)(sign | code);
+}
+
+/* weight-only quantization of bf16 rows: scale = max|w| / 448 (1 for a zero row), q = e4m3(w / scale) */
+void or_quantize_fp8(const uint16_t* src, int64_t rows, int K, uint8_t* q, float* scale) {
+#pragma omp parallel for schedule(static)
+  for (int64_t r = 0; r < rows; ++r) {
+    const uint16_t* w = src + r * K;
+    float amax = 0.0f;
+    for (int j = 0; j < K; ++j) amax = fmaxf(amax, fabsf(b2f(w[j])));
+    float sc = amax > 0.0f ? amax / 448.0f : 1.0f;
+    for (int j = 0; j < K; ++j) q[r * K + j] = e4m3_encode(b2f(w[j]) / sc);
+    scale[r] = sc;
+  }
+}
+
+/* dot_lanes over FP8 codes: chunk c = 16 contiguous codes (16 bytes) -> lane c % 64, the lane sums
+ * its chunks in increasing c (code x value is exact in FP32: mul + add == fma), the butterfly, then
+ * one multiply by the row's scale. */
+static float dot_lanes_fp8(const uint8_t* q, const float* b, int K, float scale) {
+  int nchunk = K / 16;
+  int nl = lanes_for(nchunk);
+  float acc[SPEC_LANES];
+  for (int l = 0; l < nl; ++l) acc[l] = 0.0f;
+  for (int c = 0; c < nchunk; ++c) {
+    int l = c & (SPEC_LANES - 1);
+    float s = acc[l];
+    const uint8_t* qp = q + (size_t)c * 16;
+    const float* bp = b + (size_t)c * 16;
+    for (int e = 0; e < 16; ++e) s = s + e4m3_tab[qp[e]] * bp[e];
+    acc[l] = s;
+  }
+  return butterfly(acc, nl) * scale;
+}
+
+/* or_moe_w13_silu with FP8 experts: codes Wq [slot][2I][H] and scales S [slot][2I] per slot of mask. */
+void or_moe_w13_silu_fp8(const uint16_t* h, const uint8_t* Wq, const float* S, const int32_t* mask, int n_slots,
+                         int I, int H, uint16_t* act) {
+  e4m3_init();
+  float* hf = (float*)malloc(sizeof(float) * H);
+  for (int i = 0; i < H; ++i) hf[i] = b2f(h[i]);
+  for (int s = 0; s < n_slots; ++s) {
+    int e = mask[s];
+    const uint8_t* W = Wq + (size_t)e * 2 * I * H;
+    const float* sc = S + (size_t)e * 2 * I;
+#pragma omp parallel for schedule(static)
+    for (int i = 0; i < I; ++i) {
+      float g = bf16r(dot_lanes_fp8(W + (size_t)i * H, hf, H, sc[i]));
+      float u = bf16r(dot_lanes_fp8(W + (size_t)(I + i) * H, hf, H, sc[I + i]));
+      act[(size_t)s * I + i] = f2b(or_silu(g) * u);
+    }
+  }
+  free(hf);
+}
+
+/* or_moe_w2 with FP8 experts: codes Wq [slot][H][I], scales S [slot][H]. */
+void or_moe_w2_fp8(const uint16_t* act, const uint8_t* Wq, const float* S, const int32_t* mask, int n_slots, int I,
+                   int H, uint16_t* out8) {
+  e4m3_init();
+  float* af = (float*)malloc(sizeof(float) * I);
+  for (int s = 0; s < n_slots; ++s) {
+    int e = mask[s];
+    for (int i = 0; i < I; ++i) af[i] = b2f(act[(size_t)s * I + i]);
+    const uint8_t* W = Wq + (size_t)e * H * I;
+    const float* sc = S + (size_t)e * H;
+#pragma omp parallel for schedule(static)
+    for (int n = 0; n < H; ++n) out8[(size_t)s * H + n] = f2b(dot_lanes_fp8(W + (size_t)n * I, af, I, sc[n]));
+  }
+  free(af);
+}
+
 /* out8[s][n] = bf16(dot(W2[e][n], act[s])), K = I. */
 void or_moe_w2(const uint16_t* act, const uint16_t* W2, const int32_t* mask, int n_slots, int I, int H,
                uint16_t* out8) {

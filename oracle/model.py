@@ -10,6 +10,8 @@ modeling_deepseek.py:1193-1234 (decoder layer: residual around attention and aro
 
 Weights are a mapping of the plan's packed keys (pack_weights names, suffix _l per layer) to
 uint16 arrays; a mapping may also provide .expert(key, e) to hand over one expert slab lazily.
+A mapping with fp8_experts = True provides .fp8_expert(key, e, rows, K) -> (codes uint8 [rows, K],
+scales float32 [rows]) of the FP8 expert weights (W13q_l, W2q_l) instead.
 """
 from dataclasses import dataclass
 
@@ -85,12 +87,19 @@ def layer_step(cfg, W, cache, cos, sin, x_res, step, l, rec=None):
                                                     topk=c.TOPK, n_forced=c.N_SHARED)
     n_slots = c.TOPK + c.N_SHARED
     ids = [int(e) for e in mask[:n_slots]]
-    W13 = np.stack([_expert(W, f"W13_{l}", e) for e in ids])
-    W2 = np.stack([_expert(W, f"W2_{l}", e) for e in ids])
     local = np.arange(n_slots + 1, dtype=np.int32)
     local[n_slots] = n_slots
-    act = O.moe_w13_silu(h, W13, local, n_slots)
-    out8 = O.moe_w2(act, W2, local, n_slots)
+    if getattr(W, "fp8_experts", False):
+        # FP8 expert weights: codes and per-row scales of each slot's expert
+        q13, s13 = zip(*[W.fp8_expert(f"W13q_{l}", e, 2 * c.I_MOE, c.H) for e in ids])
+        q2, s2 = zip(*[W.fp8_expert(f"W2q_{l}", e, c.H, c.I_MOE) for e in ids])
+        act = O.moe_w13_silu_fp8(h, np.stack(q13), np.stack(s13), local, n_slots)
+        out8 = O.moe_w2_fp8(act, np.stack(q2), np.stack(s2), local, n_slots)
+    else:
+        W13 = np.stack([_expert(W, f"W13_{l}", e) for e in ids])
+        W2 = np.stack([_expert(W, f"W2_{l}", e) for e in ids])
+        act = O.moe_w13_silu(h, W13, local, n_slots)
+        out8 = O.moe_w2(act, W2, local, n_slots)
     x_out = O.moe_combine(out8, topk_w, x_attn)
     if rec is not None:
         rec.update({f"L{l}.norm2": h, f"L{l}.B8.router_logits": logits, f"L{l}.B9.topk_idx": mask[:c.TOPK].copy(),

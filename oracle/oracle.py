@@ -21,6 +21,7 @@ LIB_PATH = HERE / "_build" / "liboracle.so"
 _u16p = np.ctypeslib.ndpointer(np.uint16, flags="C_CONTIGUOUS")
 _f32p = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")
 _i32p = np.ctypeslib.ndpointer(np.int32, flags="C_CONTIGUOUS")
+_u8p = np.ctypeslib.ndpointer(np.uint8, flags="C_CONTIGUOUS")
 _i64p = np.ctypeslib.ndpointer(np.int64, flags="C_CONTIGUOUS")
 _u32p = np.ctypeslib.ndpointer(np.uint32, flags="C_CONTIGUOUS")
 _vp = ctypes.c_void_p
@@ -57,6 +58,10 @@ def _load():
         "or_moe_router": (None, [_u16p, _vp, _f, _u16p, _i, _i, _i, _i, _f, _vp, _f32p, _f32p, _i32p, _i32p]),
         "or_moe_w13_silu": (None, [_u16p, _u16p, _i32p, _i, _i, _i, _u16p]),
         "or_moe_w2": (None, [_u16p, _u16p, _i32p, _i, _i, _i, _u16p]),
+        "or_e4m3_decode": (None, [_f32p]),
+        "or_quantize_fp8": (None, [_u16p, ctypes.c_int64, _i, _u8p, _f32p]),
+        "or_moe_w13_silu_fp8": (None, [_u16p, _u8p, _f32p, _i32p, _i, _i, _i, _u16p]),
+        "or_moe_w2_fp8": (None, [_u16p, _u8p, _f32p, _i32p, _i, _i, _i, _u16p]),
         "or_moe_combine": (None, [_u16p, _f32p, _u16p, _i, _i, _u16p]),
         "or_dense_mlp": (None, [_u16p, _u16p, _f, _u16p, _u16p, _i, _i, _vp, _vp, _u16p]),
         "or_argmax_bf16": (_i64, [_u16p, _i64]),
@@ -245,6 +250,42 @@ def moe_w13_silu(h, W13, mask, n_slots=8):
     act = np.zeros((n_slots, I2 // 2), np.uint16)
     lib().or_moe_w13_silu(_c(h, np.uint16), W, _c(mask, np.int32), n_slots, I2 // 2, H, act)
     return act
+
+
+def e4m3_decode():
+    """The 256 OCP e4m3fn code values (float32; NaN at 0x7F, 0xFF)."""
+    out = np.empty(256, np.float32)
+    lib().or_e4m3_decode(out)
+    return out
+
+
+def quantize_fp8(w):
+    """Weight-only FP8 of bf16 rows w [rows, K]: (codes uint8 [rows, K], scales float32 [rows]);
+    scale = max|w| / 448 (1 for a zero row), code = e4m3(w / scale), nearest even, saturated."""
+    w = _c(w, np.uint16)
+    rows, K = w.shape
+    q = np.empty((rows, K), np.uint8)
+    s = np.empty(rows, np.float32)
+    lib().or_quantize_fp8(w, rows, K, q, s)
+    return q, s
+
+
+def moe_w13_silu_fp8(h, W13q, W13s, mask, n_slots=8):
+    """moe_w13_silu with FP8 experts: codes [slots, 2I, H], scales [slots, 2I]."""
+    Wq = _c(W13q, np.uint8)
+    I2, H = Wq.shape[1], Wq.shape[2]
+    act = np.zeros((n_slots, I2 // 2), np.uint16)
+    lib().or_moe_w13_silu_fp8(_c(h, np.uint16), Wq, _c(W13s, np.float32), _c(mask, np.int32), n_slots, I2 // 2, H, act)
+    return act
+
+
+def moe_w2_fp8(act, W2q, W2s, mask, n_slots=8):
+    """moe_w2 with FP8 experts: codes [slots, H, I], scales [slots, H]."""
+    Wq = _c(W2q, np.uint8)
+    H, I = Wq.shape[1], Wq.shape[2]
+    out = np.zeros((n_slots, H), np.uint16)
+    lib().or_moe_w2_fp8(_c(act, np.uint16), Wq, _c(W2s, np.float32), _c(mask, np.int32), n_slots, I, H, out)
+    return out
 
 
 def moe_w2(act, W2, mask, n_slots=8):

@@ -49,12 +49,25 @@ class SeededCpuWeights(dict):
 
 
 class GpuWeights(dict):
-    """Packed weights downloaded from the device buffers (large tensors, one expert slab at a time)."""
+    """Packed weights downloaded from the device buffers (large tensors, one expert slab at a time).
+    With FP8 experts (W13q_l / W2q_l keys, pack_weights.quantize_experts) the oracle reads those."""
 
     def __init__(self, bufs):
         super().__init__()
         self.bufs = bufs
         self._experts = {}
+        self.fp8_experts = any(k.startswith("W13q_") for k in bufs)
+
+    def fp8_expert(self, key, e, rows, K):
+        """(codes uint8 [rows, K], scales float32 [rows]) of expert e of an FP8 key."""
+        k = (key, e)
+        if k not in self._experts:
+            buf = self.bufs[key]
+            n_exp = (buf.nbytes // (rows * (K + 4)))
+            q = buf.download_range(e * rows * K, rows * K).reshape(rows, K)
+            s = buf.download_range(n_exp * rows * K + 4 * e * rows, 4 * rows).view(np.float32)
+            self._experts[k] = (q, s)
+        return self._experts[k]
 
     def __missing__(self, key):
         v = self.bufs[key].download()

@@ -1,0 +1,72 @@
+"""FP8 expert weights on the GPU (fx_quantize_fp8, the fx_persistent_fp8 kernel variant):
+
+  * the device quantizer's codes and scales equal the oracle's quantizer on the same bf16 rows
+    (three experts of a seeded layer, W13 and W2);
+  * a 2-layer seeded model with FP8 experts decodes through the persistent kernel with the same
+    greedy ids, route ids and final hidden state as the oracle's FP8 expert path (bit-exact: the
+    FP8 dot has the oracle's lane order, code x value products are exact in FP32).
+"""
+import numpy as np
+import pytest
+
+from oracle import model as M
+from oracle import oracle as O
+from fleet import build_graph as B
+from fleet import graph_plan as G
+from fleet import pack_weights as P
+from fxtest import SEED, GpuWeights
+
+pytestmark = pytest.mark.gpu
+
+
+def test_quantizer_matches_oracle(rt):
+    d = P.REAL_DIMS
+    bufs = P.fill_seeded(rt, d, SEED, layers=2, head=False, keys={"W13_1", "W2_1"})
+    P.quantize_experts(rt, bufs, d, layers=2, free_bf16=False)
+    W = GpuWeights(bufs)
+    for key, qkey, rows, K in (("W13_1", "W13q_1", 2 * d.I_MOE, d.H), ("W2_1", "W2q_1", d.H, d.I_MOE)):
+        for e in (0, 37, d.E_TOTAL - 1):
+            print(f"[fp8] quantizer {key} expert {e}", flush=True)
+            src = bufs[key].download_range(e * rows * K, rows * K).reshape(rows, K)
+            q, s = O.quantize_fp8(src)
+            gq, gs = W.fp8_expert(qkey, e, rows, K)
+            assert np.array_equal(gq, q), (key, e, np.argwhere(gq != q)[:4])
+            assert np.array_equal(gs.view(np.uint32), s.view(np.uint32)), (key, e)
+
+
+def test_fp8_model_decode_matches_oracle(rt):
+    d = P.REAL_DIMS
+    layers, ctx, iters = 2, 24, 3
+    s_max = ctx + iters
+    bufs = P.fill_seeded(rt, d, SEED, layers=layers, head=True)
+    P.quantize_experts(rt, bufs, d, layers=layers)
+    assert "W13_1" not in bufs and "W13q_1" in bufs
+    plan = G.build_plan(d, s_max, layers, True, fp8_experts=True)
+    prompt = P.prompt_ids(SEED, ctx, d.V)
+    runner = B.build(rt, bufs, B.make_capture(rt, plan), B.make_meta(rt, s_max, prompt), d, s_max, layers, True,
+                     fp8_experts=True)
+    print(f"[fp8] decode layers={layers} ctx={ctx} iters={iters}", flush=True)
+    runner.run(ctx - 1 + iters, 0, ctx)
+    got = runner.host["tokens"].download()[ctx:ctx + iters].tolist()
+    rl = runner.host["route_log"].download()
+    x_gpu = runner.x_res()
+    cfg = M.Cfg(H=d.H, NH=d.NH, D_N=d.D_N, D_R=d.D_R, D_V=d.D_V, D_C=d.D_C, V=d.V, L=d.L, I_DENSE=d.I_DENSE,
+                I_MOE=d.I_MOE, E=d.E, TOPK=d.TOPK, N_SHARED=d.N_SHARED, eps=plan.eps, scale=plan.scale,
+                split=plan.split, n_splits=plan.n_splits)
+    cos, sin = M.rope_tables(s_max)
+    W = GpuWeights(bufs)
+    assert W.fp8_experts
+    cache = M.Cache(cfg, s_max, layers)
+    for pos in range(ctx - 1):
+        M.decode_step(cfg, W, cache, cos, sin, prompt[pos], pos, layers, head=False)
+    want, routes = [], []
+    tok, x_ref = int(prompt[-1]), None
+    for i in range(iters):
+        tok, r, x_ref = M.decode_step(cfg, W, cache, cos, sin, tok, ctx - 1 + i, layers, head=True)
+        want.append(tok)
+        routes.append(r)
+    print(f"[fp8] ids {got} oracle {want}", flush=True)
+    assert got == want
+    for i in range(iters):
+        assert sorted(rl[i, 0].tolist()) == sorted(routes[i][0]), (i, rl[i, 0].tolist(), routes[i][0])
+    assert np.array_equal(x_gpu, x_ref), int(np.count_nonzero(x_gpu != x_ref))
