@@ -34,6 +34,7 @@ def probe_lib():
     L.fxp_lanes.argtypes = [ctypes.POINTER(ctypes.c_float)]
     L.fxp_clock.argtypes = [ctypes.c_int, vp, u64, ctypes.POINTER(u64)]
     L.fxp_lds_dma.argtypes = [ctypes.POINTER(u32)]
+    L.fxp_fp8.argtypes = [ctypes.POINTER(ctypes.c_float)]
     return L
 
 
@@ -64,6 +65,18 @@ def main():
     if len(bad):
         print(got[:20], flush=True)
         sys.exit(1)
+    # the packed FP8 -> f32 conversion of the FP8 expert tiles: OCP e4m3fn (bias 7, 448 max, NaN at
+    # 0x7F / 0xFF) or the FNUZ variant (bias 8, NaN at 0x80)?
+    f8 = (ctypes.c_float * 256)()
+    assert L.fxp_fp8(f8) == 0
+    g8 = np.array(f8, np.float32)
+    c = np.arange(256)
+    e, m, neg = (c >> 3) & 15, c & 7, (c & 0x80) != 0
+    ocp = np.where(e == 0, m / 8.0 * 2.0 ** -6, (1 + m / 8.0) * 2.0 ** (e - 7.0)) * np.where(neg, -1, 1)
+    ocp[(e == 15) & (m == 7)] = np.nan
+    same = (g8 == ocp.astype(np.float32)) | (np.isnan(g8) & np.isnan(ocp))
+    print(f"FP8 conversion: {'OCP e4m3fn on all 256 codes' if same.all() else f'{(~same).sum()} codes differ from OCP e4m3fn'}"
+          f" (0x38 -> {g8[0x38]}, 0x7E -> {g8[0x7E]}, 0x01 -> {g8[0x01]})", flush=True)
     if args.lanes_only:
         return
     lines = []

@@ -1,5 +1,6 @@
 """FP8 expert weights on the GPU (fx_quantize_fp8, the fx_persistent_fp8 kernel variant):
 
+  * the hardware's packed FP8 -> f32 conversion decodes all 256 codes as OCP e4m3fn;
   * the device quantizer's codes and scales equal the oracle's quantizer on the same bf16 rows
     (three experts of a seeded layer, W13 and W2);
   * a 2-layer seeded model with FP8 experts decodes through the persistent kernel with the same
@@ -17,6 +18,18 @@ from fleet import pack_weights as P
 from fxtest import SEED, GpuWeights
 
 pytestmark = pytest.mark.gpu
+
+
+def test_hardware_fp8_conversion_is_ocp_e4m3fn(rt):
+    """v_cvt_pk_f32_fp8 (the FP8 tiles' decode) on all 256 codes equals the OCP e4m3fn table."""
+    import ctypes
+    from pathlib import Path
+    lib = ctypes.CDLL(str(Path(__file__).resolve().parent.parent / "fleet-amd-task_amd" / "lib" / "libfleet_probe.so"))
+    out = (ctypes.c_float * 256)()
+    assert lib.fxp_fp8(out) == 0
+    got = np.array(out, np.float32)
+    ref = O.e4m3_decode()
+    assert np.all((got == ref) | (np.isnan(got) & np.isnan(ref))), np.flatnonzero(got != ref)[:8]
 
 
 def test_quantizer_matches_oracle(rt):
