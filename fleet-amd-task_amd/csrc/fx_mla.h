@@ -267,7 +267,38 @@ __device__ __forceinline__ void op_mla_attend(const fx_stage& s, FxEnv& env) {
         const uint16_t* kr = buf + t * ATT_ROW;
         const uint16_t* kr2 = buf + (ATT_T + t) * ATT_ROW;
         const float* qr = ql + h * 512;
-        if (t < ntA) {
+        if (t < ntA && ntB == 0) {
+          // tile A alone (one 32-position tile in the pass): the same chains without tile B's
+#pragma unroll 4
+          for (int c = k * 128; c < k * 128 + 128; c += 8) {
+            const u32x4 kv = *(const u32x4*)(kr + c);
+            const float4 q0 = *(const float4*)(qr + c), q1 = *(const float4*)(qr + c + 4);
+            a = __builtin_fmaf(q0.x, bf_lo(kv.x), a);
+            a = __builtin_fmaf(q0.y, bf_hi(kv.x), a);
+            a = __builtin_fmaf(q0.z, bf_lo(kv.y), a);
+            a = __builtin_fmaf(q0.w, bf_hi(kv.y), a);
+            a = __builtin_fmaf(q1.x, bf_lo(kv.z), a);
+            a = __builtin_fmaf(q1.y, bf_hi(kv.z), a);
+            a = __builtin_fmaf(q1.z, bf_lo(kv.w), a);
+            a = __builtin_fmaf(q1.w, bf_hi(kv.w), a);
+          }
+          if (k == 0) {
+            const float* qpr = qp + h * 64;
+#pragma unroll
+            for (int r = 0; r < 64; r += 8) {
+              const u32x4 kv = *(const u32x4*)(kr + 512 + r);
+              const float4 q0 = *(const float4*)(qpr + r), q1 = *(const float4*)(qpr + r + 4);
+              b = __builtin_fmaf(q0.x, bf_lo(kv.x), b);
+              b = __builtin_fmaf(q0.y, bf_hi(kv.x), b);
+              b = __builtin_fmaf(q0.z, bf_lo(kv.y), b);
+              b = __builtin_fmaf(q0.w, bf_hi(kv.y), b);
+              b = __builtin_fmaf(q1.x, bf_lo(kv.z), b);
+              b = __builtin_fmaf(q1.y, bf_hi(kv.z), b);
+              b = __builtin_fmaf(q1.z, bf_lo(kv.w), b);
+              b = __builtin_fmaf(q1.w, bf_hi(kv.w), b);
+            }
+          }
+        } else if (t < ntA) {
 #pragma unroll 4
           for (int c = k * 128; c < k * 128 + 128; c += 8) {
             const u32x4 kv = *(const u32x4*)(kr + c);
@@ -406,7 +437,26 @@ __device__ __forceinline__ void op_mla_attend(const fx_stage& s, FxEnv& env) {
             pv2[u] = pB[t8 + u];
           }
         };
-        if (ntA == ATT_T && ntB == ATT_T) {
+        if (ntA == ATT_T && ntB == 0) {
+          // one full tile
+#pragma unroll
+          for (int t8 = 0; t8 < ATT_T; t8 += 8) {
+            u32x2 kv[8];
+            float pv[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+              kv[u] = *(const u32x2*)(buf + (t8 + u) * ATT_ROW + pc);
+              pv[u] = pA[t8 + u];
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+              tp[0] = __builtin_fmaf(pv[u], bf_lo(kv[u].x), tp[0]);
+              tp[1] = __builtin_fmaf(pv[u], bf_hi(kv[u].x), tp[1]);
+              tp[2] = __builtin_fmaf(pv[u], bf_lo(kv[u].y), tp[2]);
+              tp[3] = __builtin_fmaf(pv[u], bf_hi(kv[u].y), tp[3]);
+            }
+          }
+        } else if (ntA == ATT_T && ntB == ATT_T) {
           // two full tiles: no row tests
 #pragma unroll
           for (int t8 = 0; t8 < ATT_T; t8 += 8) {
