@@ -11,15 +11,20 @@ decode at batch 1. A "step" is one decoded token; `--steps` tokens are timed, st
 (so every timed token attends over 1,024..1,024+steps-1 positions), after `--warmup` untimed
 tokens at the same positions. Inputs are resident in HBM when the timed region starts.
 
-value        us per decoded token: one persistent launch per token (fx_launch, queued back to back on
-             one stream, no host wait in between); HIP events on that stream around the K launches
-             / K. Decode runs under the kernel symbol fx_persistent (a --prefill decode prefill under
-             fx_prefill, the batched one in rocBLAS and fx_pf_* kernels), so a kernel trace of this
-             command averages fx_persistent over decode tokens only
+value        us per decoded token: the K timed tokens are one persistent launch of K iterations
+             (--launch one, the default: fx_launch with iters = K, as the reference's run_fleet.py
+             decodes its 32 tokens in one mpk() call, harness/run_fleet.py:590-593); HIP events on
+             the launch's stream around it / K. --launch per-token queues K one-iteration launches
+             back to back instead (no host wait in between; each launch adds its own start-up).
+             The warmup tokens are one launch of their own before the events. Decode runs under the
+             kernel symbol fx_persistent (a --prefill decode prefill under fx_prefill, the batched
+             one in rocBLAS and fx_pf_* kernels), so a kernel trace of this command lists the
+             decode launches alone under fx_persistent
 roofline     algorithmic HBM bytes per token (every weight the token touches once -- 8 of the 66
              experts per MoE layer -- plus the latent-cache rows read and the embedding row; mean
-             over the timed tokens) / us per token, against the published 8 TB/s; traffic = the
-             measured HBM bytes per launch from the committed rocprofv3 --pmc summary
+             over the timed tokens) / us per token, against the published 8 TB/s (the same as the
+             launch's bytes / its duration); traffic = the measured HBM bytes per token from the
+             committed rocprofv3 --pmc summary x the tokens of one timed launch
 cpu_baseline the CPU oracle (oracle/, a C port of harness/numpy_ref.py semantics, OpenMP) decoding
              the first `--cpu-tokens` tokens of the same run on this host's cores, checked for
              equal ids; weights it touches are copied to host memory before its timed region
@@ -53,15 +58,16 @@ def log(*a):
     print("[bench]", *a, file=sys.stderr, flush=True)
 
 
-def traffic_bytes(ctx):
-    """HBM bytes per fx_persistent dispatch from the committed rocprofv3 --pmc summary (FETCH_SIZE and
-    WRITE_SIZE, each scaled by the same counter's reading on a copy kernel of known size), or None.
-    Counters cannot be read inside this process, so the figure comes from the profile runs."""
+def traffic_per_token(ctx):
+    """Measured HBM bytes per decoded token of fx_persistent from the committed rocprofv3 --pmc summary
+    (FETCH_SIZE and WRITE_SIZE per dispatch, each scaled by the same counter's reading on a copy kernel
+    of known size, over the dispatch's decode iterations), or None. Counters cannot be read inside
+    this process, so the figure comes from the profile runs."""
     f = ROOT / "profiles" / "fx_persistent_decode_ctx1024_traffic.json"
     if ctx != 1024 or not f.exists():
         return None
     t = json.loads(f.read_text())
-    return int(t["bytes_per_dispatch"])
+    return t["bytes_per_dispatch"] / t.get("iters_per_dispatch", 1)
 
 
 def cpu_baseline(rt, runner, bufs, plan, prompt, ctx, n_tok, gpu_ids):
@@ -145,6 +151,8 @@ def main():
     ap.add_argument("--n-splits", type=int, default=None, help="attention splits (default: 32-position splits)")
     ap.add_argument("--fp8-experts", action="store_true",
                     help="the experts' weights as FP8 (weight-only e4m3, per-row scales) instead of bf16")
+    ap.add_argument("--launch", choices=("one", "per-token"), default="one",
+                    help="the timed tokens as one launch of --steps iterations, or one launch per token")
     ap.add_argument("--prefill", choices=("batched", "decode"), default="batched",
                     help="how the untimed prefill writes the caches (batched forward pass or the decode kernel)")
     args = ap.parse_args()
@@ -192,25 +200,34 @@ def main():
     log(f"{args.prefill} prefill of {ctx - 1} positions: {prefill_s:.2f} s"
         + (f", {prefill_warm_s:.3f} s once the GEMM kernels are loaded" if prefill_warm_s else ""))
     assert K + 1 <= R.FX_MAX_MARKS, "at most 255 timed tokens"
-    for i in range(Wm):
-        runner.launch(1, ctx - 1 + i, ctx)
-    runner.finish()
     if Wm > 0:
+        runner.launch(Wm, ctx - 1, ctx)
+        runner.finish()
         log(f"warmup: {Wm} tokens")
     t0 = time.perf_counter()
     rt.mark(0)
-    for i in range(K):
-        runner.launch(1, ctx - 1 + i, ctx)
-        rt.mark(i + 1)
+    if args.launch == "one":
+        runner.launch(K, ctx - 1, ctx)
+        rt.mark(1)
+    else:
+        for i in range(K):
+            runner.launch(1, ctx - 1 + i, ctx)
+            rt.mark(i + 1)
     runner.finish()
     wall_ms = 1e3 * (time.perf_counter() - t0)
-    per_launch = [1e3 * rt.marks_ms(i, i + 1) for i in range(K)]
-    us_tok = 1e3 * rt.marks_ms(0, K) / K
+    n_marks = 1 if args.launch == "one" else K
+    us_tok = 1e3 * rt.marks_ms(0, n_marks) / K
+    # per-token times: the kernel's own iteration stamps (one launch) or the events around each launch
+    per_tok = ([float(x) for x in runner.timing_us()] if args.launch == "one"
+               else [1e3 * rt.marks_ms(i, i + 1) for i in range(K)])
     ids = runner.host["tokens"].download()[ctx:ctx + K].tolist()
     mean_bytes = sum(P.bytes_per_token(d, ctx + i, fp8_experts=args.fp8_experts) for i in range(K)) / K
     achieved = mean_bytes / (us_tok * 1e-6) / 1e9
-    log(f"decode: {us_tok:.1f} us/token (events), wall {wall_ms / K * 1e3:.1f} us/token, per-launch median "
-        f"{statistics.median(per_launch):.1f} min {min(per_launch):.1f} max {max(per_launch):.1f} us; "
+    tokens_per_launch = K if args.launch == "one" else 1
+    tpt = traffic_per_token(ctx)
+    what = "in-kernel per-iteration" if args.launch == "one" else "per-launch event"
+    log(f"decode: {us_tok:.1f} us/token (events, {args.launch} launch), wall {wall_ms / K * 1e3:.1f} us/token, "
+        f"{what} median {statistics.median(per_tok):.1f} min {min(per_tok):.1f} max {max(per_tok):.1f} us; "
         f"{achieved:.0f} GB/s = {100 * achieved / HBM_PEAK_GBPS:.1f}% of 8 TB/s")
     log(f"ids {ids}")
     out = {
@@ -225,9 +242,13 @@ def main():
                    "splits": plan.n_splits, "seed": args.seed, "fp8_experts": args.fp8_experts},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBPS, 4),
-                     "traffic": None if args.fp8_experts else traffic_bytes(ctx),
+                     "traffic": None if args.fp8_experts or tpt is None else int(tpt * tokens_per_launch),
+                     "bytes_per_launch": int(mean_bytes * tokens_per_launch), "tokens_per_launch": tokens_per_launch,
                      "bytes_per_token": int(mean_bytes), "kernel": "fx_persistent"},
-        "launch_us_median": round(statistics.median(per_launch), 2), "prefill": args.prefill,
+        "launch": args.launch, "token_us_median": round(statistics.median(per_tok), 2),
+        "token_us_source": "fx_persistent iteration stamps (s_memrealtime)" if args.launch == "one"
+                           else "HIP events around each launch",
+        "prefill": args.prefill,
         "prefill_s": round(prefill_s, 3), "prefill_warm_s": None if prefill_warm_s is None else round(prefill_warm_s, 3),
         "ids": ids,
     }
