@@ -89,8 +89,16 @@ __device__ __forceinline__ float silu_s(float x) { return x / (1.0f + exp_s(-x))
 // ------------------------------------------------------------------------------------------------
 // coherent (sc1) access to activations through buffer resources; byte offsets
 
+// The base must be the same on every lane of the wave (every caller passes a stage-table pointer or
+// a kernel argument plus a uniform offset; per-lane addressing goes in the byte offset). It is made
+// provably uniform here: the stage table lives in LDS, so its pointers arrive in vector registers,
+// and without this the compiler wraps every buffer access in a loop over the distinct bases.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* p) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, 0x7fffffff, 0x00020000);
+  const uint64_t a = (uint64_t)p;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
+  void* u = (void*)(((uint64_t)hi << 32) | lo);
+  return __builtin_amdgcn_make_buffer_rsrc(u, (short)0, 0x7fffffff, 0x00020000);
 }
 #define FX_SC1 16
 __device__ __forceinline__ u32x4 ldc16(const void* base, uint32_t off) {

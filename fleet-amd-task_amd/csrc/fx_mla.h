@@ -576,6 +576,13 @@ __device__ __forceinline__ void op_mla_merge_uv(const fx_stage& s, FxEnv& env) {
   __syncthreads();
   prof_mark(env, 1);
   const void* part = (const void*)s.x;
+  // wave 0 requests the lse of splits lane, lane + 64 first: loads complete in issue order, so the
+  // weights below need not wait for the wave's partial-o loads
+  float l0 = -__builtin_inff(), l1 = -__builtin_inff();
+  if (wave_id() == 0) {
+    if (lane_id() < live) l0 = ldcf(part, (uint32_t)((lane_id() * nh + h) * prow + d_c));
+    if (lane_id() + 64 < live) l1 = ldcf(part, (uint32_t)(((lane_id() + 64) * nh + h) * prow + d_c));
+  }
   // every thread: 2 columns of o; the first 32 splits' values are requested before anything waits
   const int pc = threadIdx.x * 2;
   u32x2 o[MERGE_BATCH];
@@ -586,10 +593,7 @@ __device__ __forceinline__ void op_mla_merge_uv(const fx_stage& s, FxEnv& env) {
   }
   // wave 0: lse_j, M = max lse, w_j = exp(lse_j - M) into LDS, den = sum_j w_j in j order
   if (wave_id() == 0) {
-    // lse of splits lane, lane + 64 (one load each), then the rest (more than 128 splits) from LDS
-    float l0 = -__builtin_inff(), l1 = -__builtin_inff();
-    if (lane_id() < live) l0 = ldcf(part, (uint32_t)((lane_id() * nh + h) * prow + d_c));
-    if (lane_id() + 64 < live) l1 = ldcf(part, (uint32_t)(((lane_id() + 64) * nh + h) * prow + d_c));
+    // the rest of the lse (more than 128 splits) from LDS
     float mx = fmaxf(l0, l1);
     for (int j = lane_id() + 128; j < live; j += 64) {
       const float v = ldcf(part, (uint32_t)((j * nh + h) * prow + d_c));
