@@ -248,7 +248,9 @@ __device__ __forceinline__ void store_vec_sc1(void* dst, const float* xs, int K)
 
 // rmsnorm in place on xs (harness/numpy_ref.py:54-60): var = dot_lanes(x, x) / K,
 // rs = 1 / sqrt(var + eps), y = bf16(w * bf16(x * rs)). Starts and ends with __syncthreads.
-__device__ __forceinline__ void rmsnorm_inplace(float* xs, const uint16_t* wn, int K, float eps, float* red) {
+// wchunk(i): the 8 bf16 norm weights of elements i .. i + 8.
+template <class WChunk>
+__device__ __forceinline__ void rmsnorm_body(float* xs, int K, float eps, float* red, WChunk wchunk) {
   __syncthreads();
   if (wave_id() == 0) {
     float ss = sumsq_wave(xs, K);
@@ -261,7 +263,7 @@ __device__ __forceinline__ void rmsnorm_inplace(float* xs, const uint16_t* wn, i
   const float rs = red[0];
   for (int i = threadIdx.x * 8; i < K; i += FX_THREADS * 8) {
     float w8[8];
-    unpack8(ld16(wn + i), w8);
+    unpack8(wchunk(i), w8);
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       float xn = bf16r(xs[i + e] * rs);
@@ -269,6 +271,29 @@ __device__ __forceinline__ void rmsnorm_inplace(float* xs, const uint16_t* wn, i
     }
   }
   __syncthreads();
+}
+__device__ __forceinline__ void rmsnorm_inplace(float* xs, const uint16_t* wn, int K, float eps, float* red) {
+  rmsnorm_body(xs, K, eps, red, [&](int i) { return ld16(wn + i); });
+}
+// The same with the norm weights requested ahead (norm_prefetch, before the stage polls its input:
+// their load latency then hides under the wait instead of following the input). K <= 8 * FX_THREADS:
+// thread t's only chunk is elements 8t .. 8t + 8.
+struct NormW {
+  u32x4 w;
+};
+__device__ __forceinline__ NormW norm_prefetch(const uint16_t* wn, int K) {
+  NormW n;
+  n.w = u32x4{0u, 0u, 0u, 0u};
+  if (threadIdx.x * 8 < K) n.w = ld16(wn + threadIdx.x * 8);
+  return n;
+}
+__device__ __forceinline__ void rmsnorm_pre(float* xs, const NormW& n, int K, float eps, float* red) {
+  rmsnorm_body(xs, K, eps, red, [&](int) { return n.w; });
+}
+// either, by K
+__device__ __forceinline__ void rmsnorm_staged(float* xs, const NormW& n, const uint16_t* wn, int K, float eps, float* red) {
+  if (K <= 8 * FX_THREADS) rmsnorm_pre(xs, n, K, eps, red);
+  else rmsnorm_inplace(xs, wn, K, eps, red);
 }
 
 // greedy id from the per-worker (max, index) packet pairs: the lowest index among the maxima (one
@@ -339,6 +364,8 @@ __device__ __forceinline__ void op_gemv_t(const fx_stage& s, FxEnv& env) {
   auto rowof = [&](int g, int i) { const int r = r0 + g * R + i; return r < r1 ? r : -1; };
   Tile<R, NJ> t0;
   gemv_prime(t0, W, K, ngroups, rowof);
+  const bool norm = (s.flags & FX_F_NORM) != 0;
+  const NormW nw = norm && K <= 8 * FX_THREADS ? norm_prefetch((const uint16_t*)s.w_norm, K) : NormW{};
   const bool out_ll = (s.flags & FX_F_OUT_LL) != 0;
   const bool residual = (s.flags & FX_F_RESIDUAL) != 0;
   const bool res_embed = (s.flags & FX_F_RES_EMBED) != 0;
@@ -364,7 +391,7 @@ __device__ __forceinline__ void op_gemv_t(const fx_stage& s, FxEnv& env) {
     for (int i = threadIdx.x; i < r1 - r0; i += FX_THREADS) rres[i] = bf2f(erow[r0 + i]);
   }
   prof_mark(env, 1);
-  if (s.flags & FX_F_NORM) rmsnorm_inplace(xs, (const uint16_t*)s.w_norm, K, s.eps, red);
+  if (norm) rmsnorm_staged(xs, nw, (const uint16_t*)s.w_norm, K, s.eps, red);
   else __syncthreads();
   // ---- rows
   void* out = (void*)s.out;
@@ -466,9 +493,10 @@ __device__ __forceinline__ void op_dense_gu(const fx_stage& s, FxEnv& env) {
   const int ngroups = q1 - q0;
   Tile<4, 4> t0;
   gemv_prime(t0, W, K, ngroups, rowof);
+  const NormW nw = K <= 8 * FX_THREADS ? norm_prefetch((const uint16_t*)s.w_norm, K) : NormW{};
   poll_row(xs, (const void*)s.x, K, tag_in(s, env, 0), env.err);
   prof_mark(env, 1);
-  rmsnorm_inplace(xs, (const uint16_t*)s.w_norm, K, s.eps, red);
+  rmsnorm_staged(xs, nw, (const uint16_t*)s.w_norm, K, s.eps, red);
   if (s.aux[6] && env.worker == 0) store_vec_sc1((void*)s.aux[6], xs, K);
   void* act = (void*)s.out;
   const uint32_t tag = tag_out(env);

@@ -73,6 +73,7 @@ __device__ __forceinline__ void op_mla_prep(const fx_stage& s, FxEnv& env) {
   float* rp = red + 512;                          // roped k_pe [64], q_pe [2][64]
   const uint16_t* cosr = (const uint16_t*)s.aux[3] + (size_t)env.step * d_r;
   const uint16_t* sinr = (const uint16_t*)s.aux[4] + (size_t)env.step * d_r;
+  const NormW nw = d_c <= 8 * FX_THREADS ? norm_prefetch((const uint16_t*)s.w_norm, d_c) : NormW{};
   {
     // pairs: latent (q_out .. q_out + d_c) -> 128, k_pe -> 16, q_pe of the two heads -> 2 x 16
     const int t = threadIdx.x;
@@ -95,7 +96,7 @@ __device__ __forceinline__ void op_mla_prep(const fx_stage& s, FxEnv& env) {
     }
   }
   prof_mark(env, 1);
-  rmsnorm_inplace(xs, (const uint16_t*)s.w_norm, d_c, s.eps, red);
+  rmsnorm_staged(xs, nw, (const uint16_t*)s.w_norm, d_c, s.eps, red);
   if (threadIdx.x < d_r * (1 + MLA_HP)) {
     const int v = threadIdx.x / d_r, i = threadIdx.x % d_r;
     rp[threadIdx.x] = rope64(kp + 64 * v, cosr, sinr, i);

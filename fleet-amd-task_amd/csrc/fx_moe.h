@@ -67,9 +67,10 @@ __device__ __forceinline__ void op_moe_router(const fx_stage& s, FxEnv& env) {
   auto rowof = [&](int g, int i) { return e; };
   Tile<1, 4> t0;
   gemv_prime(t0, W, K, 1, rowof);
+  const NormW nw = K <= 8 * FX_THREADS ? norm_prefetch((const uint16_t*)s.w_norm, K) : NormW{};
   poll_row(xs, (const void*)s.x, K, tag_in(s, env, 0), env.err);
   prof_mark(env, 1);
-  rmsnorm_inplace(xs, (const uint16_t*)s.w_norm, K, s.eps, red);
+  rmsnorm_staged(xs, nw, (const uint16_t*)s.w_norm, K, s.eps, red);
   const uint32_t tag = tag_out(env);
   gemv_pipe(t0, W, K, xs, 1, rowof, [&](int g, const int* row, const float* acc) {
     if (lane_id() == 0) pk_put((void*)s.out, (uint32_t)e, __float_as_uint(acc[0]), tag);
@@ -121,9 +122,10 @@ __device__ __forceinline__ void op_moe_w13_t(const fx_stage& s, FxEnv& env, cons
   auto rowR = [&](int g, int i) { return env.worker; };
   Tile<1, 4> tr;
   if (rrow && wave_id() == 0) tile_load(tr, Wg, K, 0, rowR);
+  const NormW nw = K <= 8 * FX_THREADS ? norm_prefetch((const uint16_t*)s.w_norm, K) : NormW{};
   poll_row(xs, (const void*)s.x, K, tag_in(s, env, 1), env.err);
   prof_mark(env, 1);
-  rmsnorm_inplace(xs, (const uint16_t*)s.w_norm, K, s.eps, red);
+  rmsnorm_staged(xs, nw, (const uint16_t*)s.w_norm, K, s.eps, red);
   const uint32_t tag = tag_out(env);
   if (rrow && wave_id() == 0) {
     float acc[1];
