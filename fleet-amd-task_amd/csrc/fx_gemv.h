@@ -14,6 +14,7 @@
 template <int R, int NJ>
 struct Tile {
   static constexpr int kRows = R;
+  using Row = Tile<1, NJ>;   // one row of the same chunking
   u32x4 w[R][NJ];
   int row[R];
 };
@@ -28,6 +29,7 @@ struct Fp8W {
 template <int R, int NJ>
 struct TileQ {
   static constexpr int kRows = R;
+  using Row = TileQ<1, NJ>;
   u32x4 w[R][NJ];
   int row[R];
   float sc[R];
@@ -393,6 +395,7 @@ __device__ __forceinline__ void op_gemv_t(const fx_stage& s, FxEnv& env) {
   prof_mark(env, 1);
   if (norm) rmsnorm_staged(xs, nw, (const uint16_t*)s.w_norm, K, s.eps, red);
   else __syncthreads();
+  prof_mark(env, 4);
   // ---- rows
   void* out = (void*)s.out;
   const bool want_max = (s.flags & FX_F_ARGMAX) != 0;
@@ -418,6 +421,7 @@ __device__ __forceinline__ void op_gemv_t(const fx_stage& s, FxEnv& env) {
       }
     }
   });
+  prof_mark(env, 5);
   if (out_ll) {
     __syncthreads();
     const float* o = rres + FX_MAX_OUT_ROWS / 2;

@@ -10,12 +10,16 @@
 
 // rope of one 64-vector (i in [0, 64)): de-interleave the (even, odd) pairs, x*cos + rotate_half(x)*sin,
 // bf16 at every op (harness/numpy_ref.py:63-71, HF modeling_deepseek.py:339-371)
-__device__ __forceinline__ float rope64(const float* xin, const uint16_t* cosr, const uint16_t* sinr, int i) {
+// element i with its table entries c = cos[i], sn = sin[i] already read
+__device__ __forceinline__ float rope64_cs(const float* xin, float c, float sn, int i) {
   const float xd = i < 32 ? xin[2 * i] : xin[2 * (i - 32) + 1];
   const float rot = i < 32 ? -xin[2 * i + 1] : xin[2 * (i - 32)];
-  const float a = bf16r(xd * bf2f(cosr[i]));
-  const float b = bf16r(rot * bf2f(sinr[i]));
+  const float a = bf16r(xd * c);
+  const float b = bf16r(rot * sn);
   return bf16r(a + b);
+}
+__device__ __forceinline__ float rope64(const float* xin, const uint16_t* cosr, const uint16_t* sinr, int i) {
+  return rope64_cs(xin, bf2f(cosr[i]), bf2f(sinr[i]), i);
 }
 
 // FX_OP_MLA_PREP (harness/numpy_ref.py:85-103). Per XCD: 32 wave tasks of ql_nope (head, 32
@@ -74,6 +78,13 @@ __device__ __forceinline__ void op_mla_prep(const fx_stage& s, FxEnv& env) {
   const uint16_t* cosr = (const uint16_t*)s.aux[3] + (size_t)env.step * d_r;
   const uint16_t* sinr = (const uint16_t*)s.aux[4] + (size_t)env.step * d_r;
   const NormW nw = d_c <= 8 * FX_THREADS ? norm_prefetch((const uint16_t*)s.w_norm, d_c) : NormW{};
+  // this thread's RoPE table entries (k_pe and the two q_pe rows), also requested ahead of the input
+  const bool roper = threadIdx.x < d_r * (1 + MLA_HP);
+  float rc = 0.0f, rsn = 0.0f;
+  if (roper) {
+    rc = bf2f(cosr[threadIdx.x % d_r]);
+    rsn = bf2f(sinr[threadIdx.x % d_r]);
+  }
   {
     // pairs: latent (q_out .. q_out + d_c) -> 128, k_pe -> 16, q_pe of the two heads -> 2 x 16
     const int t = threadIdx.x;
@@ -97,9 +108,9 @@ __device__ __forceinline__ void op_mla_prep(const fx_stage& s, FxEnv& env) {
   }
   prof_mark(env, 1);
   rmsnorm_staged(xs, nw, (const uint16_t*)s.w_norm, d_c, s.eps, red);
-  if (threadIdx.x < d_r * (1 + MLA_HP)) {
+  if (roper) {
     const int v = threadIdx.x / d_r, i = threadIdx.x % d_r;
-    rp[threadIdx.x] = rope64(kp + 64 * v, cosr, sinr, i);
+    rp[threadIdx.x] = rope64_cs(kp + 64 * v, rc, rsn, i);
   }
   __syncthreads();
   if (env.xcd == 0) {

@@ -197,12 +197,35 @@ __device__ __forceinline__ void op_moe_w13_t(const fx_stage& s, FxEnv& env, cons
   // the routing stays in LDS for the expert-down stage that follows on this worker
   env.route_tag = router ? tag : tag_in(s, env, 0);
   prof_mark(env, 6);
-  gemv_prime(t0, W, K, nB, rowB);
-  gemv_pipe(t0, W, K, xs, nB, rowB, [&](int g, const int* row, const float* acc) { emit(nA, g, acc); });
+  // The routed groups are walked by whole waves up to a multiple of the wave count; one group left
+  // over (the split gives every other worker 17 at V2-Lite's shapes) is split by rows, row w on wave
+  // w, its loads requested ahead of the walk: the worker then ends a quarter tile after its
+  // 16-group neighbours instead of a whole tile. Each row's dot is the same as in a 4-row tile.
+  const int nrem = nB % FX_WAVES;
+  const int nB4 = nrem == 1 && TileT::kRows == FX_WAVES ? nB - 1 : nB;
+  float* remv = red + 896;   // the split group's 4 row values
+  typename TileT::Row tq;
+  auto rowQ = [&](int, int) { return rowB(nB4, wave_id()); };
+  if (nB4 < nB) tile_load(tq, W, K, 0, rowQ);
+  gemv_prime(t0, W, K, nB4, rowB);
+  gemv_pipe(t0, W, K, xs, nB4, rowB, [&](int g, const int* row, const float* acc) { emit(nA, g, acc); });
+  if (nB4 < nB) {
+    float acc[1];
+    tile_dot(tq, xs, K, acc);
+    if (lane_id() == 0) remv[wave_id()] = acc[0];
+  }
   __syncthreads();
   if (threadIdx.x < nB) {
     const int r = b0 + threadIdx.x;
     const int i = nA + threadIdx.x;
+    if (threadIdx.x == nB4) {
+      // rows gate p, up p, gate p + 1, up p + 1 of the split group: emit's arithmetic
+      float a[2];
+#pragma unroll
+      for (int q = 0; q < 2; ++q) a[q] = silu_s(bf16r(remv[2 * q])) * bf16r(remv[2 * q + 1]);
+      actl[2 * i] = a[0];
+      actl[2 * i + 1] = a[1];
+    }
     pk_put(act, (uint32_t)((r / PG) * half + r % PG), pack2(actl[2 * i], actl[2 * i + 1]), tag);
   }
   prof_mark(env, 2);

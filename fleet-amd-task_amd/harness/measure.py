@@ -74,7 +74,8 @@ def report(rows, d, ctx, iter_us=None):
         lines += ["", "Operator-internal points (median over workers, µs after the worker's inputs arrived):",
                   "attention: 4 first tile scored, 5 softmaxed, 6 value product done, 7 partials complete; "
                   "merge: 4 lse weights, 5 merged o; w13: 4 normed (+ router row), 5 shared slots done, 6 top-k "
-                  "known; w2: 4 shared slots done, 5 routed activations arrived", "", "| stage | 4 | 5 | 6 | 7 |", "|---|---|---|---|---|"]
+                  "known; w2: 4 shared slots done, 5 routed activations arrived; GEMV (qkva, o_proj, dense down, LM head): "
+                  "4 input normed, 5 rows done", "", "| stage | 4 | 5 | 6 | 7 |", "|---|---|---|---|---|"]
         for r in marked[:16]:
             cells = " | ".join("-" if m is None else f"{m:.2f}" for m in r["marks"])
             lines.append(f"| {r['label']} | {cells} |")
