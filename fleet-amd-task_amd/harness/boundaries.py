@@ -205,6 +205,26 @@ def write(path, tensors, metadata=None):
             f.write(raw)
 
 
+def read_raw(path):
+    """{name: (safetensors dtype, numpy array)} of a safetensors file with the stored bits kept:
+    BF16 tensors come back as their uint16 bit patterns (the bit-diff report reads these)."""
+    data = Path(path).read_bytes()
+    n = struct.unpack("<Q", data[:8])[0]
+    header = json.loads(data[8:8 + n])
+    base = 8 + n
+    out = {}
+    for name, t in header.items():
+        if name == "__metadata__":
+            continue
+        a, e = t["data_offsets"]
+        dt = np.uint16 if t["dtype"] == "BF16" else _DT_READ.get(t["dtype"])
+        if dt is None:
+            raise TypeError(f"{name}: safetensors dtype {t['dtype']} not supported")
+        arr = np.frombuffer(data[base + a:base + e], np.dtype(dt).newbyteorder("<")).astype(dt)
+        out[name] = (t["dtype"], arr.reshape(t["shape"]))
+    return out
+
+
 def read(path):
     """{name: numpy array} of a safetensors file; BF16 tensors come back as float32 (exact)."""
     data = Path(path).read_bytes()

@@ -74,3 +74,24 @@ def test_run_fleet_then_compare(rt, tmp_path):
     # this build is bit-exact with the oracle at every boundary
     assert all(r.get("rel_err", 0.0) == 0.0 for r in rows), [(r["key"], r["rel_err"]) for r in rows if r.get("rel_err")]
     assert res["overall"] == "PASS" and res["n_not_comparable"] == 0
+
+
+def test_bitdiff_of_two_runs_is_zero(rt, tmp_path):
+    """bitdiff.py over two run_fleet dumps of the same seeded run: every boundary key on both sides,
+    no element differs (the decode is deterministic to the bit)."""
+    import bitdiff as BDIFF
+    dirs = []
+    for name in ("a", "b"):
+        out = tmp_path / name
+        print(f"[bitdiff] run_fleet into {out}", flush=True)
+        meta = RF.run(RF.build_parser().parse_args(["--layers", "2", "--head", "--iters", "2", "--ctx", "24",
+                                                    "--out", str(out)]), rt=rt)
+        assert meta["completed"]
+        dirs.append(out)
+    text = BDIFF.run(*dirs, out=tmp_path / "bitdiff.md")
+    rows = [l for l in text.splitlines() if l.startswith("| `")]
+    assert len(rows) >= 20, text
+    assert "only in" not in text, text
+    for l in rows:
+        c = [x.strip() for x in l.split("|")[1:-1]]
+        assert c[3] == "0" and c[4] == "0", l
