@@ -88,8 +88,15 @@ def cpu_baseline(rt, runner, bufs, plan, prompt, ctx, n_tok, gpu_ids):
     cos, sin = M.rope_tables(plan.s_max)
     # host copies of every weight the sampled tokens touch (routes from the GPU run's route log)
     W = {}
-    for key in ("W_embed", "W_lm", "w_final_norm"):
+    for key in ("W_embed", "w_final_norm"):
         W[key] = bufs[key].download()
+    head_q = None
+    if plan.fp8_head:
+        buf = bufs["W_lmq"]
+        head_q = (buf.download_range(0, d.V * d.H).reshape(d.V, d.H),
+                  buf.download_range(d.V * d.H, 4 * d.V).view(np.float32))
+    else:
+        W["W_lm"] = bufs["W_lm"].download()
     for l in range(d.L):
         for key in (f"w_norm1_{l}", f"w_norm2_{l}", f"W_qkva_{l}", f"w_kv_norm_{l}", f"W_uk_{l}", f"W_uv_{l}", f"W_o_{l}"):
             W[key] = bufs[key].download()
@@ -116,6 +123,10 @@ def cpu_baseline(rt, runner, bufs, plan, prompt, ctx, n_tok, gpu_ids):
 
     class HostW(dict):
         fp8_experts = fp8
+        fp8_head = plan.fp8_head
+
+        def fp8_rows(self, key, rows, K):
+            return head_q
 
         def expert(self, key, e):
             return experts[(key, e)]
@@ -151,6 +162,7 @@ def main():
     ap.add_argument("--n-splits", type=int, default=None, help="attention splits (default: 32-position splits)")
     ap.add_argument("--fp8-experts", action="store_true",
                     help="the experts' weights as FP8 (weight-only e4m3, per-row scales) instead of bf16")
+    ap.add_argument("--fp8-head", action="store_true", help="the LM head's weights as FP8 too (implies --fp8-experts)")
     ap.add_argument("--launch", choices=("one", "per-token"), default="one",
                     help="the timed tokens as one launch of --steps iterations, or one launch per token")
     ap.add_argument("--prefill", choices=("batched", "decode"), default="batched",
@@ -174,14 +186,20 @@ def main():
     gen_s = time.time() - t0
     log(f"seeded weights: {P.packed_bytes(d) / 2**30:.2f} GiB in {gen_s:.1f} s")
     prompt = P.prompt_ids(args.seed, ctx, d.V)
+    if args.fp8_head:
+        args.fp8_experts = True
     if args.fp8_experts:
         t0 = time.time()
         P.quantize_experts(rt, bufs, d, d.L)
-        log(f"FP8 experts: quantized in {time.time() - t0:.1f} s")
-    plan = G.build_plan(d, s_max, d.L, True, n_splits=args.n_splits, fp8_experts=args.fp8_experts)
+        if args.fp8_head:
+            P.quantize_head(rt, bufs, d)
+        log(f"FP8 experts{' and LM head' if args.fp8_head else ''}: quantized in {time.time() - t0:.1f} s")
+    plan = G.build_plan(d, s_max, d.L, True, n_splits=args.n_splits, fp8_experts=args.fp8_experts,
+                        fp8_head=args.fp8_head)
     meta = B.make_meta(rt, s_max, prompt)
     cap = B.make_capture(rt, plan)
-    runner = B.build(rt, bufs, cap, meta, d, s_max, d.L, True, n_splits=args.n_splits, fp8_experts=args.fp8_experts)
+    runner = B.build(rt, bufs, cap, meta, d, s_max, d.L, True, n_splits=args.n_splits, fp8_experts=args.fp8_experts,
+                     fp8_head=args.fp8_head)
     log(f"plan: {len(runner.stages)} stages/iteration, {plan.n_splits} splits of {plan.split}, s_max {s_max}")
     t0 = time.time()
     prefill_warm_s = None
@@ -221,7 +239,8 @@ def main():
     per_tok = ([float(x) for x in runner.timing_us()] if args.launch == "one"
                else [1e3 * rt.marks_ms(i, i + 1) for i in range(K)])
     ids = runner.host["tokens"].download()[ctx:ctx + K].tolist()
-    mean_bytes = sum(P.bytes_per_token(d, ctx + i, fp8_experts=args.fp8_experts) for i in range(K)) / K
+    mean_bytes = sum(P.bytes_per_token(d, ctx + i, fp8_experts=args.fp8_experts, fp8_head=args.fp8_head)
+                     for i in range(K)) / K
     achieved = mean_bytes / (us_tok * 1e-6) / 1e9
     tokens_per_launch = K if args.launch == "one" else 1
     tpt = traffic_per_token(ctx)
@@ -233,13 +252,16 @@ def main():
     out = {
         "metric": METRIC, "value": round(us_tok, 2), "unit": "µs/token", "n_gpus": 1, "steps": K, "warmup": Wm,
         "ms_per_step": round(us_tok / 1e3, 5), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
-        "dtype": "fp8-e4m3 expert weights x bf16" if args.fp8_experts else "bf16",
-        "data": "synthetic: seeded N(0,0.02) bf16 weights" + (" (experts quantized to FP8, per-row scales)"
-                                                              if args.fp8_experts else "")
+        "dtype": ("fp8-e4m3 expert and LM head weights x bf16" if args.fp8_head else
+                  "fp8-e4m3 expert weights x bf16" if args.fp8_experts else "bf16"),
+        "data": "synthetic: seeded N(0,0.02) bf16 weights" + (
+            " (experts and LM head quantized to FP8, per-row scales)" if args.fp8_head else
+            " (experts quantized to FP8, per-row scales)" if args.fp8_experts else "")
                 + ", seeded uniform 1024-token prompt",
         "config": {"workload": "BASELINE configs[3]: DeepSeek-V2-Lite 27 layers, 1024-token prompt (prefill untimed), "
                                "greedy decode at batch 1", "layers": d.L, "batch": 1, "ctx": ctx, "decode_tokens": K,
-                   "splits": plan.n_splits, "seed": args.seed, "fp8_experts": args.fp8_experts},
+                   "splits": plan.n_splits, "seed": args.seed, "fp8_experts": args.fp8_experts,
+                   "fp8_head": args.fp8_head},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBPS, 4),
                      "traffic": None if args.fp8_experts or tpt is None else int(tpt * tokens_per_launch),

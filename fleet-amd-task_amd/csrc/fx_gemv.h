@@ -351,20 +351,20 @@ __device__ __forceinline__ void embed_token(const void* amax, uint32_t amax_tag,
 #ifndef FX_GEMV_R
 #define FX_GEMV_R 4
 #endif
-template <int NJ>
-__device__ __forceinline__ void op_gemv_t(const fx_stage& s, FxEnv& env) {
-  constexpr int R = NJ <= 4 ? FX_GEMV_R : 1;
+// TileT / WT: bf16 tiles over a bf16 matrix, or FP8 tiles over codes + per-row scales (Fp8W)
+template <class TileT, class WT>
+__device__ __forceinline__ void op_gemv_w(const fx_stage& s, FxEnv& env, const WT& W) {
+  constexpr int R = TileT::kRows;
   float* xs = (float*)(env.lds + LDS_XS);
   float* red = (float*)(env.lds + LDS_RED);
   float* rres = (float*)(env.lds + LDS_RES);
-  const uint16_t* W = (const uint16_t*)s.w;
   const int K = s.k;
   int g0, g1;
   range_split((s.n_rows + 3) >> 2, env.nworkers, env.worker, g0, g1);
   const int r0 = g0 * 4, r1 = g1 * 4 < s.n_rows ? g1 * 4 : s.n_rows;
   const int ngroups = (r1 - r0 + R - 1) / R;
   auto rowof = [&](int g, int i) { const int r = r0 + g * R + i; return r < r1 ? r : -1; };
-  Tile<R, NJ> t0;
+  TileT t0;
   gemv_prime(t0, W, K, ngroups, rowof);
   const bool norm = (s.flags & FX_F_NORM) != 0;
   const NormW nw = norm && K <= 8 * FX_THREADS ? norm_prefetch((const uint16_t*)s.w_norm, K) : NormW{};
@@ -443,6 +443,19 @@ __device__ __forceinline__ void op_gemv_t(const fx_stage& s, FxEnv& env) {
     }
   }
   prof_mark(env, 2);
+}
+
+template <int NJ>
+__device__ __forceinline__ void op_gemv_t(const fx_stage& s, FxEnv& env) {
+  constexpr int R = NJ <= 4 ? FX_GEMV_R : 1;
+  op_gemv_w<Tile<R, NJ>>(s, env, (const uint16_t*)s.w);
+}
+
+// FX_F_FP8 (the LM head of an FP8 plan): w = the codes [n_rows][K] then one f32 scale per row;
+// K <= 2048 (two 16-code chunks per lane); tiles of 8 rows, 16 KiB per wave as a bf16 tile of 4
+__device__ __forceinline__ void op_gemv_fp8(const fx_stage& s, FxEnv& env) {
+  const Fp8W W{(const uint8_t*)s.w, (const float*)((const uint8_t*)s.w + (size_t)s.n_rows * (size_t)s.k)};
+  op_gemv_w<TileQ<8, 2>>(s, env, W);
 }
 
 __device__ __forceinline__ void op_gemv(const fx_stage& s, FxEnv& env) {

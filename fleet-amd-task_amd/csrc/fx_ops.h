@@ -13,7 +13,12 @@
 template <bool kFp8 = false>
 __device__ __forceinline__ void run_stage(const fx_stage& s, FxEnv& env) {
   switch (s.op) {
-    case FX_OP_GEMV: op_gemv(s, env); break;
+    case FX_OP_GEMV:
+      if constexpr (kFp8) {
+        if (s.flags & FX_F_FP8) { op_gemv_fp8(s, env); break; }
+      }
+      op_gemv(s, env);
+      break;
     case FX_OP_MLA_PREP: op_mla_prep(s, env); break;
     case FX_OP_MLA_ATTEND: op_mla_attend(s, env); break;
     case FX_OP_MLA_MERGE_UV: op_mla_merge_uv(s, env); break;

@@ -385,7 +385,9 @@ static int check_stage(fx_ctx* c, const fx_stage& s, int idx, int n_total) {
   for (int k = 0; k < 4; ++k)
     if (s.src[k] < -n_total || s.src[k] >= n_total) return bad("packet source out of range");
   if (s.flags & FX_F_FP8) {
-    if (s.op != FX_OP_MOE_W13 && s.op != FX_OP_MOE_W2) return bad("FP8 weights are read by the expert stages only");
+    const bool head = s.op == FX_OP_GEMV && (s.flags & FX_F_ARGMAX) && s.in_kind == FX_IN_VEC;
+    if (s.op != FX_OP_MOE_W13 && s.op != FX_OP_MOE_W2 && !head)
+      return bad("FP8 weights are read by the expert stages and the LM head only");
     if (s.k % 16 || (s.k / 16 + 63) / 64 > 2) return bad("FP8 K must be a multiple of 16, at most 2048");
   }
   switch (s.op) {
@@ -476,6 +478,12 @@ int fx_load_plan(fx_ctx* c, const fx_stage* st, int32_t n, const fx_stage* epi, 
       n_fp8 += (st[i].flags & FX_F_FP8) != 0;
     }
   if (n_fp8 && n_fp8 != n_exp) return fail(c, FX_E_ARG, "a plan's expert stages must be all bf16 or all FP8");
+  // an FP8 LM head runs in the FP8 kernel variant, which the launch picks from the expert stages
+  for (int i = 0; i < n + n_epi; ++i) {
+    const fx_stage& t = i < n ? st[i] : epi[i - n];
+    if (t.op == FX_OP_GEMV && (t.flags & FX_F_FP8) && (n_exp == 0 || n_fp8 != n_exp))
+      return fail(c, FX_E_ARG, "an FP8 LM head needs FP8 expert stages in the same plan");
+  }
   if (c->d_stages) { HIPCHK(c, hipFree(c->d_stages)); c->d_stages = nullptr; }
   if (c->d_epi) { HIPCHK(c, hipFree(c->d_epi)); c->d_epi = nullptr; }
   HIPCHK(c, hipMalloc(&c->d_stages, sizeof(fx_stage) * n));

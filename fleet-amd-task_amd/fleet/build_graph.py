@@ -78,10 +78,12 @@ def compile_stages(plan, host):
         common = dict(layer=layer, eps=plan.eps)
         if m == "linear_gemv_layer":
             W = host[a["weight"]]
-            st = _stage(op=R.FX_OP_GEMV, n_rows=W.shape[0], k=W.shape[1], w=W.ptr, out=B(a["output"]),
+            fp8 = plan.fp8_head and a.get("amax") is not None
+            rows_k = (d.V, d.H) if fp8 else (W.shape[0], W.shape[1])
+            st = _stage(op=R.FX_OP_GEMV, n_rows=rows_k[0], k=rows_k[1], w=W.ptr, out=B(a["output"]),
                         in_kind=R.FX_IN_VEC, **common)
             ins = []
-            flags = 0
+            flags = R.FX_F_FP8 if fp8 else 0
             if host[a["output"]].dtype == "pk16":
                 flags |= R.FX_F_OUT_LL
             if a.get("norm"):
@@ -323,6 +325,7 @@ def build(rt, packed, capture, meta, dims: Dims = REAL_DIMS, s_max=1056, layers=
 def plan_json(plan):
     return {"dims": plan.dims.__dict__, "s_max": plan.s_max, "layers": plan.layers, "head": plan.head,
             "split": plan.split, "n_splits": plan.n_splits, "fp8_experts": plan.fp8_experts,
+            "fp8_head": plan.fp8_head,
             "calls": [{"method": c.method, "label": c.label, "tasks": c.tasks,
                        "args": {k: v for k, v in c.args.items() if isinstance(v, (str, int, float, bool)) or v is None}}
                       for c in plan.calls]}

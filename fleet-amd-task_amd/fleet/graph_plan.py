@@ -84,6 +84,7 @@ class Plan:
     tensors: dict = field(default_factory=dict)
     calls: list = field(default_factory=list)
     fp8_experts: bool = False   # W13 / W2 are FP8 (codes + per-row scales, pack_weights.quantize_experts)
+    fp8_head: bool = False      # W_lm is FP8 too (pack_weights.quantize_head; needs fp8_experts)
 
     def t(self, name, shape, dtype="bf16", kind="new", source=""):
         assert name not in self.tensors, name
@@ -153,7 +154,7 @@ def default_splits(s_max):
 
 def build_plan(dims: Dims = REAL_DIMS, s_max: int = 1056, layers: int = 27, head: bool = True, split: int = None,
                n_splits: int = None, iters_cap: int = 32, softmax_scale: float = SOFTMAX_SCALE,
-               eps: float = RMS_EPS, fp8_experts: bool = False) -> Plan:
+               eps: float = RMS_EPS, fp8_experts: bool = False, fp8_head: bool = False) -> Plan:
     """split / n_splits: the attention split (positions) or split count; neither: default_splits."""
     d = dims
     assert 1 <= layers <= d.L
@@ -162,6 +163,8 @@ def build_plan(dims: Dims = REAL_DIMS, s_max: int = 1056, layers: int = 27, head
     p.scale = softmax_scale
     p.eps = eps
     p.fp8_experts = fp8_experts
+    assert fp8_experts or not fp8_head, "an FP8 LM head runs in the FP8 kernel variant: fp8_experts too"
+    p.fp8_head = fp8_head
     p.iters_cap = iters_cap
     # ---- meta and shared tensors
     p.t("tokens", (s_max + 1,), "i64", "input", "meta:tokens")
@@ -243,7 +246,10 @@ def build_plan(dims: Dims = REAL_DIMS, s_max: int = 1056, layers: int = 27, head
                  input="out8", weight="topk_w", residual="x_mid", output="x_res")
     if head:
         p.t("w_final_norm", (d.H,), kind="input", source="w_final_norm")
-        p.t("W_lm", (d.V, d.H), kind="input", source="W_lm")
+        if fp8_head:
+            p.t("W_lm", (fp8_nbytes(d, "W_lm"),), "u8", kind="input", source="W_lmq")
+        else:
+            p.t("W_lm", (d.V, d.H), kind="input", source="W_lm")
         p.t("logits", (d.V,))
         p.op("linear_gemv_layer", WORKERS, "head.lm_head", input="x_res", w_norm="w_final_norm",
              weight="W_lm", residual=None, output="logits", amax="amax", norm=True)

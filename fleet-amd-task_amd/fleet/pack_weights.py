@@ -222,11 +222,11 @@ def packed_bytes(d: Dims = REAL_DIMS):
 
 
 def bytes_per_token(d: Dims = REAL_DIMS, ctx: int = 1024, layers: int = None, head: bool = True,
-                    fp8_experts: bool = False):
+                    fp8_experts: bool = False, fp8_head: bool = False):
     """Algorithmic HBM bytes of one decode step attending over `ctx` positions (positions 0..ctx-1):
     every weight the step touches once (8 of the 66 experts per MoE layer) plus the latent-cache rows
     read, plus the embedding row. Activations (KBs) are not counted. fp8_experts: the experts' weights
-    at one byte each plus one f32 scale per row."""
+    at one byte each plus one f32 scale per row; fp8_head: the LM head likewise."""
     L = d.L if layers is None else layers
     attn = (d.Q_OUT + d.KVA_OUT) * d.H + d.KVB_OUT * d.D_C + d.H * d.NH * d.D_V + 2 * d.H + d.D_C
     moe = d.E * d.H + d.N_SLOTS * 3 * d.I_MOE * d.H
@@ -235,7 +235,7 @@ def bytes_per_token(d: Dims = REAL_DIMS, ctx: int = 1024, layers: int = None, he
     dense = 3 * d.I_DENSE * d.H
     w = L * attn + (dense if L >= 1 else 0) + max(0, L - 1) * moe + d.H
     if head:
-        w += d.V * d.H + d.H
+        w += (d.V * d.H + 4 * d.V) // 2 + d.H if fp8_head else d.V * d.H + d.H
     kv = L * ctx * (d.D_C + d.D_R)
     return 2 * (w + kv)
 
@@ -262,7 +262,10 @@ def fill_seeded(rt, d: Dims = REAL_DIMS, seed: int = 0, layers: int = None, head
 # ---- FP8 expert weights ---------------------------------------------------------------------------
 
 def fp8_rows(d: Dims, key: str):
-    """(rows, K) of the FP8 form of a W13 / W2 packed key (rows over all E + N_SHARED experts)."""
+    """(rows, K) of the FP8 form of a W13 / W2 packed key (rows over all E + N_SHARED experts) or of
+    the LM head W_lm."""
+    if key.startswith("W_lm"):
+        return d.V, d.H
     if key.startswith("W13"):
         return d.E_TOTAL * 2 * d.I_MOE, d.H
     return d.E_TOTAL * d.H, d.I_MOE
@@ -289,6 +292,19 @@ def quantize_experts(rt, bufs, d: Dims, layers: int = None, free_bf16: bool = Tr
                 rt.synchronize()
                 bufs.pop(key).free()
     rt.synchronize()
+    return bufs
+
+
+def quantize_head(rt, bufs, d: Dims, free_bf16: bool = True):
+    """Add W_lmq (the LM head as FP8 codes + per-row scales, fx_quantize_fp8, as quantize_experts)
+    from the bf16 W_lm in `bufs`; W_lm is freed unless free_bf16 is False. Returns bufs."""
+    rows, K = fp8_rows(d, "W_lm")
+    q = rt.alloc((fp8_nbytes(d, "W_lm"),), "u8")
+    rt.check(rt.L.fx_quantize_fp8(rt.h, bufs["W_lm"].ptr, q.ptr, rows, K, None), "fx_quantize_fp8")
+    bufs["W_lmq"] = q
+    rt.synchronize()
+    if free_bf16:
+        bufs.pop("W_lm").free()
     return bufs
 
 

@@ -111,7 +111,8 @@ enum fx_op {
 #define FX_F_OUT_LL 32u    /* output as packets */
 #define FX_F_RES_EMBED 64u /* residual = the embedding row of this iteration's token */
 #define FX_F_ROUTER 128u   /* MOE_W13 computes the router itself (W_gate in res) */
-#define FX_F_FP8 256u      /* MOE_W13 / MOE_W2: w is FP8 (OCP e4m3fn codes, then one f32 scale per row) */
+#define FX_F_FP8 256u      /* MOE_W13 / MOE_W2, or the LM head GEMV (FX_F_ARGMAX) of a plan whose expert stages
+                            * are FP8: w is FP8 (OCP e4m3fn codes [rows][k], then one f32 scale per row) */
 
 /* One entry of the task table: one operator of the plan (fleet/graph_plan.py Call). */
 typedef struct fx_stage {

@@ -545,6 +545,24 @@ static float dot_lanes_fp8(const uint8_t* q, const float* b, int K, float scale)
   return butterfly(acc, nl) * scale;
 }
 
+/* or_linear with FP8 weights (the LM head of an FP8 plan): codes Wq [N][K], scales S [N];
+ * out[n] = bf16(dot_lanes_fp8(Wq[n], x', S[n])), x' = rmsnorm(x, norm_w) when norm_w is given. */
+void or_linear_fp8(const uint8_t* Wq, const float* S, const uint16_t* x, const uint16_t* norm_w, float eps, int64_t N,
+                   int K, uint16_t* out, uint16_t* h_out) {
+  e4m3_init();
+  float* xf = (float*)malloc(sizeof(float) * K);
+  if (norm_w) {
+    rmsnorm_f(x, norm_w, K, eps, xf);
+    if (h_out)
+      for (int i = 0; i < K; ++i) h_out[i] = f2b(xf[i]);
+  } else {
+    for (int i = 0; i < K; ++i) xf[i] = b2f(x[i]);
+  }
+#pragma omp parallel for schedule(static)
+  for (int64_t n = 0; n < N; ++n) out[n] = f2b(dot_lanes_fp8(Wq + (size_t)n * K, xf, K, S[n]));
+  free(xf);
+}
+
 /* or_moe_w13_silu with FP8 experts: codes Wq [slot][2I][H] and scales S [slot][2I] per slot of mask. */
 void or_moe_w13_silu_fp8(const uint16_t* h, const uint8_t* Wq, const float* S, const int32_t* mask, int n_slots,
                          int I, int H, uint16_t* act) {

@@ -120,7 +120,11 @@ def decode_step(cfg, W, cache, cos, sin, token, step, layers=None, head=True, re
             routes.append(ids)
     if not head:
         return None, routes, x
-    logits, hf = O.linear(W["W_lm"], x, norm_w=W["w_final_norm"], eps=cfg.eps)
+    if getattr(W, "fp8_head", False):
+        q, sc = W.fp8_rows("W_lmq", cfg.V, cfg.H)
+        logits, hf = O.linear_fp8(q, sc, x, norm_w=W["w_final_norm"], eps=cfg.eps)
+    else:
+        logits, hf = O.linear(W["W_lm"], x, norm_w=W["w_final_norm"], eps=cfg.eps)
     tok = O.argmax_bf16(logits)
     if rec is not None:
         rec.update({"head.B14.norm": hf, "head.B15.logits": logits, "head.B16.token": np.array([tok], np.int64)})

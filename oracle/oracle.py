@@ -60,6 +60,7 @@ def _load():
         "or_moe_w2": (None, [_u16p, _u16p, _i32p, _i, _i, _i, _u16p]),
         "or_e4m3_decode": (None, [_f32p]),
         "or_quantize_fp8": (None, [_u16p, ctypes.c_int64, _i, _u8p, _f32p]),
+        "or_linear_fp8": (None, [_u8p, _f32p, _u16p, _vp, _f, _i64, _i, _u16p, _vp]),
         "or_moe_w13_silu_fp8": (None, [_u16p, _u8p, _f32p, _i32p, _i, _i, _i, _u16p]),
         "or_moe_w2_fp8": (None, [_u16p, _u8p, _f32p, _i32p, _i, _i, _i, _u16p]),
         "or_moe_combine": (None, [_u16p, _f32p, _u16p, _i, _i, _u16p]),
@@ -268,6 +269,18 @@ def quantize_fp8(w):
     s = np.empty(rows, np.float32)
     lib().or_quantize_fp8(w, rows, K, q, s)
     return q, s
+
+
+def linear_fp8(Wq, S, x, norm_w=None, eps=1e-6):
+    """linear() with FP8 weights (codes Wq [N, K], per-row scales S [N]): out[n] =
+    bf16(dot_lanes16(codes, x') * S[n]), x' the normalised row when norm_w is given. Returns (out, h)."""
+    Wq, x = _c(Wq, np.uint8), _c(x, np.uint16)
+    N, K = Wq.shape
+    out = np.empty(N, np.uint16)
+    nw = _c(norm_w, np.uint16) if norm_w is not None else None
+    h = np.empty(K, np.uint16) if norm_w is not None else None
+    lib().or_linear_fp8(Wq, _c(S, np.float32), x, _ptr(nw), eps, N, K, out, _ptr(h))
+    return out, h
 
 
 def moe_w13_silu_fp8(h, W13q, W13s, mask, n_slots=8):

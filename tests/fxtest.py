@@ -57,6 +57,7 @@ class GpuWeights(dict):
         self.bufs = bufs
         self._experts = {}
         self.fp8_experts = any(k.startswith("W13q_") for k in bufs)
+        self.fp8_head = "W_lmq" in bufs
 
     def fp8_expert(self, key, e, rows, K):
         """(codes uint8 [rows, K], scales float32 [rows]) of expert e of an FP8 key."""
@@ -66,6 +67,16 @@ class GpuWeights(dict):
             n_exp = (buf.nbytes // (rows * (K + 4)))
             q = buf.download_range(e * rows * K, rows * K).reshape(rows, K)
             s = buf.download_range(n_exp * rows * K + 4 * e * rows, 4 * rows).view(np.float32)
+            self._experts[k] = (q, s)
+        return self._experts[k]
+
+    def fp8_rows(self, key, rows, K):
+        """(codes uint8 [rows, K], scales float32 [rows]) of a whole FP8 matrix (the LM head)."""
+        k = (key, None)
+        if k not in self._experts:
+            buf = self.bufs[key]
+            q = buf.download_range(0, rows * K).reshape(rows, K)
+            s = buf.download_range(rows * K, 4 * rows).view(np.float32)
             self._experts[k] = (q, s)
         return self._experts[k]
 

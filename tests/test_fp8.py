@@ -70,3 +70,32 @@ def test_fp8_bytes_per_token():
     scales = (d.L - 1) * d.N_SLOTS * (2 * d.I_MOE + d.H) * 4
     assert b16 - b8 == experts - scales
     assert P.fp8_nbytes(d, "W13_1") == d.E_TOTAL * 2 * d.I_MOE * (d.H + 4)
+
+
+def test_fp8_linear_against_float64():
+    """The FP8 LM head's linear (rmsnorm prologue, dot over codes x row, the row's scale, bf16): float64
+    on the dequantized codes within the FP32 summation bound; exact on small integers; the normalised
+    row equals the bf16 linear's."""
+    rng = np.random.default_rng(11)
+    N, K = 96, 2048
+    w = P.f32_to_bf16((rng.standard_normal((N, K)) * 0.02).astype(np.float32))
+    x = P.f32_to_bf16(rng.standard_normal(K).astype(np.float32))
+    nw = P.f32_to_bf16((1 + 0.1 * rng.standard_normal(K)).astype(np.float32))
+    q, s = O.quantize_fp8(w)
+    out, h = O.linear_fp8(q, s, x, norm_w=nw, eps=1e-6)
+    _, h_bf = O.linear(w, x, norm_w=nw, eps=1e-6)
+    assert np.array_equal(h, h_bf)
+    tab = O.e4m3_decode().astype(np.float64)
+    hv = P.bf16_to_f32(h).astype(np.float64)
+    ref = (tab[q] @ hv) * s.astype(np.float64)
+    got = P.bf16_to_f32(out).astype(np.float64)
+    bound = 2.0 ** -8 * np.abs(ref) + 2.0 ** -22 * (np.abs(tab[q]) @ np.abs(hv)) * s + 1e-30
+    assert (np.abs(got - ref) <= bound).all(), np.max(np.abs(got - ref) / bound)
+    # a wrong scale row would be caught: rows differ in scale by construction
+    assert len(np.unique(s)) >= 16
+    # exact case: codes 1.0 (0x38) and 2.0 (0x40), integer inputs, scale 1 -> the exact integer sum
+    qe = np.where(rng.random((4, 64)) < 0.5, 0x38, 0x40).astype(np.uint8)
+    xe = P.f32_to_bf16(rng.integers(-8, 9, 64).astype(np.float32))
+    oe, _ = O.linear_fp8(qe, np.ones(4, np.float32), xe)
+    want = tab[qe] @ P.bf16_to_f32(xe).astype(np.float64)
+    assert np.array_equal(P.bf16_to_f32(oe).astype(np.float64), want)

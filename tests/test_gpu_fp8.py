@@ -3,9 +3,9 @@
   * the hardware's packed FP8 -> f32 conversion decodes all 256 codes as OCP e4m3fn;
   * the device quantizer's codes and scales equal the oracle's quantizer on the same bf16 rows
     (three experts of a seeded layer, W13 and W2);
-  * a 2-layer seeded model with FP8 experts decodes through the persistent kernel with the same
-    greedy ids, route ids and final hidden state as the oracle's FP8 expert path (bit-exact: the
-    FP8 dot has the oracle's lane order, code x value products are exact in FP32).
+  * a 2-layer seeded model with FP8 experts (and FP8 experts + FP8 LM head) decodes through the
+    persistent kernel with the same greedy ids, route ids and final hidden state as the oracle's FP8
+    path (bit-exact: the FP8 dot has the oracle's lane order, code x value products are exact in FP32).
 """
 import numpy as np
 import pytest
@@ -47,18 +47,30 @@ def test_quantizer_matches_oracle(rt):
             assert np.array_equal(gs.view(np.uint32), s.view(np.uint32)), (key, e)
 
 
-def test_fp8_model_decode_matches_oracle(rt):
+@pytest.mark.parametrize("fp8_head", [False, True])
+def test_fp8_model_decode_matches_oracle(rt, fp8_head):
+    """FP8 experts (and, with fp8_head, the FP8 LM head): ids, routes and the final hidden row equal the
+    oracle's FP8 path bit for bit."""
     d = P.REAL_DIMS
     layers, ctx, iters = 2, 24, 3
     s_max = ctx + iters
     bufs = P.fill_seeded(rt, d, SEED, layers=layers, head=True)
     P.quantize_experts(rt, bufs, d, layers=layers)
     assert "W13_1" not in bufs and "W13q_1" in bufs
-    plan = G.build_plan(d, s_max, layers, True, fp8_experts=True)
+    if fp8_head:
+        P.quantize_head(rt, bufs, d, free_bf16=False)
+        # the device quantizer's head codes and scales equal the oracle's on the first and last rows
+        q, sc = GpuWeights(bufs).fp8_rows("W_lmq", d.V, d.H)
+        for r0 in (0, d.V - 256):
+            src = bufs["W_lm"].download_range(r0 * d.H, 256 * d.H).reshape(256, d.H)
+            qq, ss = O.quantize_fp8(src)
+            assert np.array_equal(q[r0:r0 + 256], qq) and np.array_equal(sc[r0:r0 + 256], ss), r0
+        bufs.pop("W_lm").free()
+    plan = G.build_plan(d, s_max, layers, True, fp8_experts=True, fp8_head=fp8_head)
     prompt = P.prompt_ids(SEED, ctx, d.V)
     runner = B.build(rt, bufs, B.make_capture(rt, plan), B.make_meta(rt, s_max, prompt), d, s_max, layers, True,
-                     fp8_experts=True)
-    print(f"[fp8] decode layers={layers} ctx={ctx} iters={iters}", flush=True)
+                     fp8_experts=True, fp8_head=fp8_head)
+    print(f"[fp8] decode layers={layers} ctx={ctx} iters={iters} fp8_head={fp8_head}", flush=True)
     runner.run(ctx - 1 + iters, 0, ctx)
     got = runner.host["tokens"].download()[ctx:ctx + iters].tolist()
     rl = runner.host["route_log"].download()
@@ -68,7 +80,7 @@ def test_fp8_model_decode_matches_oracle(rt):
                 split=plan.split, n_splits=plan.n_splits)
     cos, sin = M.rope_tables(s_max)
     W = GpuWeights(bufs)
-    assert W.fp8_experts
+    assert W.fp8_experts and W.fp8_head == fp8_head
     cache = M.Cache(cfg, s_max, layers)
     for pos in range(ctx - 1):
         M.decode_step(cfg, W, cache, cos, sin, prompt[pos], pos, layers, head=False)
