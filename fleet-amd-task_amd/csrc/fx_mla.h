@@ -281,7 +281,7 @@ __device__ __forceinline__ void op_mla_attend(const fx_stage& s, FxEnv& env) {
         const float* qr = ql + h * 512;
         if (t < ntA && ntB == 0) {
           // tile A alone (one 32-position tile in the pass): the same chains without tile B's
-#pragma unroll 4
+#pragma unroll 8
           for (int c = k * 128; c < k * 128 + 128; c += 8) {
             const u32x4 kv = *(const u32x4*)(kr + c);
             const float4 q0 = *(const float4*)(qr + c), q1 = *(const float4*)(qr + c + 4);
@@ -311,7 +311,7 @@ __device__ __forceinline__ void op_mla_attend(const fx_stage& s, FxEnv& env) {
             }
           }
         } else if (t < ntA) {
-#pragma unroll 4
+#pragma unroll 8
           for (int c = k * 128; c < k * 128 + 128; c += 8) {
             const u32x4 kv = *(const u32x4*)(kr + c);
             const u32x4 kv2 = *(const u32x4*)(kr2 + c);
