@@ -327,6 +327,48 @@ __global__ void fxp_lds_dma_kernel(const uint32_t* src, uint32_t* dst) {
   for (int i = lane; i < 512; i += 64) dst[i] = buf[i];
 }
 
+// ---- MFMA bf16 semantics: case = blockIdx.x, one wave runs one v_mfma_f32_16x16x32_bf16 on
+// A[case] [16][32], B[case] [32][16] (k rows), C[case] [16][16] and stores D[case] [16][16]. The
+// assumed operand layout: lane l holds A[l % 16][8 (l / 16) + i] and B[8 (l / 16) + i][l % 16] for
+// i < 8, C and D [4 (l / 16) + j][l % 16] for j < 4 (checked by exact integer cases on the host).
+typedef __bf16 fxp_bf16x8 __attribute__((ext_vector_type(8)));
+typedef float fxp_f32x4 __attribute__((ext_vector_type(4)));
+__global__ void fxp_mfma_kernel(const uint16_t* A, const uint16_t* B, const float* C, float* D) {
+  const size_t cs = blockIdx.x;
+  const int l = threadIdx.x & 63, r = l & 15, g = l >> 4;
+  const uint16_t* a = A + cs * 512;
+  const uint16_t* b = B + cs * 512;
+  fxp_bf16x8 av, bv;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    av[i] = __builtin_bit_cast(__bf16, a[r * 32 + 8 * g + i]);
+    bv[i] = __builtin_bit_cast(__bf16, b[(8 * g + i) * 16 + r]);
+  }
+  fxp_f32x4 cv;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) cv[j] = C[cs * 256 + (4 * g + j) * 16 + r];
+  const fxp_f32x4 dv = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bv, cv, 0, 0, 0);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) D[cs * 256 + (4 * g + j) * 16 + r] = dv[j];
+}
+
+// ---- LDS transpose read: LDS holds u16 index values lds[i] = i (8 KiB); lane l issues
+// ds_read_b64_tr_b16 at byte offset off[l] (8-byte aligned, < 8 KiB - 8); out[l][0..3] = what it got
+typedef short fxp_i16x4 __attribute__((ext_vector_type(4)));
+__global__ void fxp_ldstr_kernel(const uint32_t* off, uint16_t* out) {
+  __shared__ __attribute__((aligned(16))) uint16_t buf[4096];
+  const int l = threadIdx.x & 63;
+  for (int i = l; i < 4096; i += 64) buf[i] = (uint16_t)i;
+  __syncthreads();
+  uint32_t o = off[l];
+  if (o > 8192 - 8) o = 0;
+  o &= ~7u;
+  const fxp_i16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) fxp_i16x4*)(
+      (__attribute__((address_space(3))) char*)(void*)buf + o));
+#pragma unroll
+  for (int j = 0; j < 4; ++j) out[l * 4 + j] = (uint16_t)v[j];
+}
+
 extern "C" {
 
 // all functions: 0 on success, else the hipError_t value
@@ -444,6 +486,47 @@ int fxp_lds_dma(uint32_t* out_host) {
   e = hipMemcpy(out_host, dst, 2048, hipMemcpyDeviceToHost);
   (void)hipFree(src);
   (void)hipFree(dst);
+  return e;
+}
+
+// n_cases MFMA cases (host arrays: A, B n_cases * 512 bf16 bits, C, D n_cases * 256 f32)
+int fxp_mfma(const uint16_t* A, const uint16_t* B, const float* C, float* D, int n_cases) {
+  if (n_cases <= 0 || n_cases > (1 << 20)) return (int)hipErrorInvalidValue;
+  uint16_t *dA = nullptr, *dB = nullptr;
+  float *dC = nullptr, *dD = nullptr;
+  hipError_t e;
+  const size_t n = (size_t)n_cases;
+  if ((e = hipMalloc(&dA, n * 1024)) != hipSuccess) return e;
+  if ((e = hipMalloc(&dB, n * 1024)) != hipSuccess) return e;
+  if ((e = hipMalloc(&dC, n * 1024)) != hipSuccess) return e;
+  if ((e = hipMalloc(&dD, n * 1024)) != hipSuccess) return e;
+  if ((e = hipMemcpy(dA, A, n * 1024, hipMemcpyHostToDevice)) != hipSuccess) return e;
+  if ((e = hipMemcpy(dB, B, n * 1024, hipMemcpyHostToDevice)) != hipSuccess) return e;
+  if ((e = hipMemcpy(dC, C, n * 1024, hipMemcpyHostToDevice)) != hipSuccess) return e;
+  hipLaunchKernelGGL(fxp_mfma_kernel, dim3(n_cases), dim3(64), 0, 0, (const uint16_t*)dA, (const uint16_t*)dB,
+                     (const float*)dC, dD);
+  if ((e = hipDeviceSynchronize()) != hipSuccess) return e;
+  e = hipMemcpy(D, dD, n * 1024, hipMemcpyDeviceToHost);
+  (void)hipFree(dA);
+  (void)hipFree(dB);
+  (void)hipFree(dC);
+  (void)hipFree(dD);
+  return e;
+}
+
+// one wave of ds_read_b64_tr_b16 at the 64 byte offsets off_host; out_host: 64 x 4 u16
+int fxp_ldstr(const uint32_t* off_host, uint16_t* out_host) {
+  uint32_t* d_off = nullptr;
+  uint16_t* d_out = nullptr;
+  hipError_t e;
+  if ((e = hipMalloc(&d_off, 256)) != hipSuccess) return e;
+  if ((e = hipMalloc(&d_out, 512)) != hipSuccess) return e;
+  if ((e = hipMemcpy(d_off, off_host, 256, hipMemcpyHostToDevice)) != hipSuccess) return e;
+  hipLaunchKernelGGL(fxp_ldstr_kernel, dim3(1), dim3(64), 0, 0, (const uint32_t*)d_off, d_out);
+  if ((e = hipDeviceSynchronize()) != hipSuccess) return e;
+  e = hipMemcpy(out_host, d_out, 512, hipMemcpyDeviceToHost);
+  (void)hipFree(d_off);
+  (void)hipFree(d_out);
   return e;
 }
 

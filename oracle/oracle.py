@@ -48,12 +48,15 @@ def _load():
         "or_f32_to_bf16": (ctypes.c_uint16, [_f]),
         "or_round_bf16_array": (None, [_f32p, _u16p, _i64]),
         "or_dot_lanes": (_f, [_u16p, _u16p, _i]),
+        "or_mfma_dot32": (_f, [_u16p, _u16p, _i, _f]),
+        "or_mfma_cases": (None, [_u16p, _u16p, _f32p, _f32p, _i64]),
         "or_rmsnorm": (None, [_u16p, _u16p, _i, _f, _u16p]),
         "or_rope": (None, [_u16p, _u16p, _u16p, _i, _u16p]),
         "or_linear": (None, [_u16p, _u16p, _vp, _f, _vp, _i64, _i, _u16p, _vp]),
         "or_linear_f32": (None, [_u16p, _u16p, _i64, _i, _f32p]),
         "or_mla_prep": (None, [_u16p, _u16p, _u16p, _u16p, _u16p, _i, _i, _i, _i, _f, _u16p, _u16p, _u16p, _u16p]),
         "or_mla_attend": (None, [_u16p, _u16p, _u16p, _u16p, _i, _f, _i, _i, _i, _i, _i, _i, _f32p, _vp, _i]),
+        "or_mla_attend_mfma": (None, [_u16p, _u16p, _u16p, _u16p, _i, _f, _i, _i, _i, _i, _i, _i, _f32p]),
         "or_mla_merge_uv": (None, [_f32p, _u16p, _i, _i, _i, _i, _i, _i, _u16p, _vp]),
         "or_moe_router": (None, [_u16p, _vp, _f, _u16p, _i, _i, _i, _i, _f, _vp, _f32p, _f32p, _i32p, _i32p]),
         "or_moe_w13_silu": (None, [_u16p, _u16p, _i32p, _i, _i, _i, _u16p]),
@@ -135,6 +138,25 @@ def silu_s(x):
     return y
 
 
+def mfma_cases(A, B, C):
+    """gfx950 v_mfma_f32_16x16x32_bf16 per case: D = A B + C with the instruction's own
+    accumulation (fleet_oracle.c, or_mfma_dot32). A [n, 16, 32], B [n, 32, 16] bf16 bits, C f32."""
+    A, B = _c(A, np.uint16), _c(B, np.uint16)
+    C = _c(C, np.float32)
+    n = A.shape[0]
+    assert A.shape == (n, 16, 32) and B.shape == (n, 32, 16) and C.shape == (n, 16, 16)
+    D = np.empty((n, 16, 16), np.float32)
+    lib().or_mfma_cases(A.reshape(-1), B.reshape(-1), C.reshape(-1), D.reshape(-1), n)
+    return D
+
+
+def mfma_dot32(a, b, c=0.0):
+    """One output of the instruction: c + sum_k a[k] b[k] over 32 bf16 pairs."""
+    a, b = _c(a, np.uint16), _c(b, np.uint16)
+    assert a.size == 32 and b.size == 32
+    return np.float32(lib().or_mfma_dot32(a, b, 1, float(c)))
+
+
 def dot_lanes(a, b):
     a, b = _c(a, np.uint16), _c(b, np.uint16)
     return np.float32(lib().or_dot_lanes(a, b, a.size))
@@ -214,6 +236,22 @@ def mla_attend(ql_nope, q_pe, c_kv, k_pe, step, softmax_scale, split=32, n_split
     lib().or_mla_attend(ql, qp, ck, kp, step, softmax_scale, split, n_splits, nh, d_c, d_r, prow, part,
                         _ptr(scores), s_max)
     return (part, scores) if with_scores else part
+
+
+def mla_attend_mfma(ql_nope, q_pe, c_kv, k_pe, step, softmax_scale, split=32, n_splits=None):
+    """numpy_ref.mla_attend (numpy_ref.py:110-149) in the matrix-core order of the gfx950 kernel
+    (fleet_oracle.c, or_mla_attend_mfma): partials [n_splits, nh, prow] f32."""
+    ql, qp = _c(ql_nope, np.uint16), _c(q_pe, np.uint16)
+    ck, kp = _c(c_kv, np.uint16), _c(k_pe, np.uint16)
+    nh, d_c = ql.shape
+    d_r = qp.shape[1]
+    assert (d_c + d_r) % 32 == 0 and split % 32 == 0
+    s_max = ck.shape[0]
+    n_splits = n_splits or -(-s_max // split)
+    prow = partials_row(d_c)
+    part = np.zeros((n_splits, nh, prow), np.float32)
+    lib().or_mla_attend_mfma(ql, qp, ck, kp, step, softmax_scale, split, n_splits, nh, d_c, d_r, prow, part)
+    return part
 
 
 def mla_merge_uv(partials, W_uv, step, split=32):
