@@ -78,9 +78,7 @@ def cpu_baseline(rt, runner, bufs, plan, prompt, ctx, n_tok, gpu_ids):
     from oracle import model as M
 
     d = plan.dims
-    cfg = M.Cfg(H=d.H, NH=d.NH, D_N=d.D_N, D_R=d.D_R, D_V=d.D_V, D_C=d.D_C, V=d.V, L=d.L, I_DENSE=d.I_DENSE,
-                I_MOE=d.I_MOE, E=d.E, TOPK=d.TOPK, N_SHARED=d.N_SHARED, eps=plan.eps, scale=plan.scale,
-                split=plan.split, n_splits=plan.n_splits)
+    cfg = M.cfg_for_plan(plan)
     cache = M.Cache(cfg, plan.s_max)
     for l in range(d.L):
         cache.c_kv[l][:ctx - 1] = runner.host[f"c_kv_{l}"].download()[:ctx - 1]
@@ -159,7 +157,10 @@ def main():
     ap.add_argument("--seed", type=int, default=20261201)
     ap.add_argument("--cpu-tokens", type=int, default=16)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--n-splits", type=int, default=None, help="attention splits (default: 32-position splits)")
+    ap.add_argument("--n-splits", type=int, default=None, help="attention split count (default: the plan's own)")
+    ap.add_argument("--split", type=int, default=None, help="attention split length in positions (a multiple of 32)")
+    ap.add_argument("--attn", choices=("mfma", "valu"), default="mfma",
+                    help="attention kernel: matrix cores over all workers (mfma) or vector-ALU chains per XCD (valu)")
     ap.add_argument("--fp8-experts", action="store_true",
                     help="the experts' weights as FP8 (weight-only e4m3, per-row scales) instead of bf16")
     ap.add_argument("--fp8-head", action="store_true", help="the LM head's weights as FP8 too (implies --fp8-experts)")
@@ -194,12 +195,12 @@ def main():
         if args.fp8_head:
             P.quantize_head(rt, bufs, d)
         log(f"FP8 experts{' and LM head' if args.fp8_head else ''}: quantized in {time.time() - t0:.1f} s")
-    plan = G.build_plan(d, s_max, d.L, True, n_splits=args.n_splits, fp8_experts=args.fp8_experts,
-                        fp8_head=args.fp8_head)
+    plan_kw = dict(split=args.split, n_splits=args.n_splits, fp8_experts=args.fp8_experts, fp8_head=args.fp8_head,
+                   attn=args.attn)
+    plan = G.build_plan(d, s_max, d.L, True, **plan_kw)
     meta = B.make_meta(rt, s_max, prompt)
     cap = B.make_capture(rt, plan)
-    runner = B.build(rt, bufs, cap, meta, d, s_max, d.L, True, n_splits=args.n_splits, fp8_experts=args.fp8_experts,
-                     fp8_head=args.fp8_head)
+    runner = B.build(rt, bufs, cap, meta, d, s_max, d.L, True, **plan_kw)
     log(f"plan: {len(runner.stages)} stages/iteration, {plan.n_splits} splits of {plan.split}, s_max {s_max}")
     t0 = time.time()
     prefill_warm_s = None
@@ -260,7 +261,7 @@ def main():
                 + ", seeded uniform 1024-token prompt",
         "config": {"workload": "BASELINE configs[3]: DeepSeek-V2-Lite 27 layers, 1024-token prompt (prefill untimed), "
                                "greedy decode at batch 1", "layers": d.L, "batch": 1, "ctx": ctx, "decode_tokens": K,
-                   "splits": plan.n_splits, "seed": args.seed, "fp8_experts": args.fp8_experts,
+                   "splits": plan.n_splits, "split": plan.split, "attn": plan.attn, "seed": args.seed, "fp8_experts": args.fp8_experts,
                    "fp8_head": args.fp8_head},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBPS, 4),
@@ -283,6 +284,10 @@ def main():
         except Exception as e:  # the baseline is reported, never the measured value
             out["cpu_baseline"] = {"value": None, "error": repr(e)}
     print(json.dumps(out), flush=True)
+    # explicit teardown (every device buffer freed, then the context destroyed) before the
+    # interpreter exits, so no HIP call runs during its finalisation
+    del runner, bufs, cap, meta
+    rt.close()
 
 
 if __name__ == "__main__":

@@ -209,6 +209,37 @@ __device__ __forceinline__ void pk_wait_pairs(const void* base, int first, int s
   }
 }
 
+// Poll the single packets first + n * stride (n < N, index < npkts) until each carries `tag`
+// (every round issues the loads of all pending packets before checking any of them).
+template <int N>
+__device__ __forceinline__ void pk_wait_singles(const void* base, int first, int stride, int npkts, uint32_t tag,
+                                                uint32_t* err) {
+  uint32_t pending = 0;
+#pragma unroll
+  for (int n = 0; n < N; ++n)
+    if (first + n * stride < npkts) pending |= 1u << n;
+  uint64_t t0 = 0;
+  for (uint32_t round = 0; pending != 0u; ++round) {
+    u32x2 v[N];
+#pragma unroll
+    for (int n = 0; n < N; ++n)
+      if (pending & (1u << n)) v[n] = ldc8(base, (uint32_t)(first + n * stride) * 8u);
+#pragma unroll
+    for (int n = 0; n < N; ++n)
+      if ((pending & (1u << n)) && v[n].y == tag) pending &= ~(1u << n);
+    if (pending == 0u) break;
+    if (round == 0) t0 = __builtin_amdgcn_s_memrealtime();
+    __builtin_amdgcn_s_sleep(1);
+    if ((round & 15u) == 15u) {
+      if (__builtin_amdgcn_s_memrealtime() - t0 > FX_TIMEOUT_TICKS) {
+        __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        break;
+      }
+      if (__hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) break;
+    }
+  }
+}
+
 // one packet (any index): payload
 __device__ __forceinline__ uint32_t pk_wait1(const void* base, uint32_t pkt, uint32_t tag, uint32_t* err) {
   u32x2 v = ldc8(base, pkt * 8u);

@@ -578,8 +578,13 @@ __device__ __forceinline__ void op_mla_merge_uv(const fx_stage& s, FxEnv& env) {
   const int ngroups = (nrows + 3) / 4;
   Tile<4, 1> t0;
   gemv_prime(t0, W, d_c, ngroups, rowof);
-  // the XCD's 32 done packets
-  if (wave_id() == 0) {
+  if (s.flags & FX_F_MFMA) {
+    // split j ran on worker j % 256: the done packets of workers 0 .. min(live, 256) - 1
+    if (wave_id() == 0)
+      pk_wait_singles<4>((const void*)s.aux[6], lane_id(), 64, live < FX_WORKERS ? live : FX_WORKERS,
+                         tag_in(s, env, 0), env.err);
+  } else if (wave_id() == 0) {
+    // the XCD's 32 done packets
     u32x4 v[1];
     const int first = env.xcd * FX_XWORKERS / 2;
     pk_wait_pairs<1>((const void*)s.aux[6], first + (lane_id() & 15), 0, first + FX_XWORKERS / 2, tag_in(s, env, 0),

@@ -4,8 +4,9 @@
 //   fx_gemv.h  GEMV (qkva, o_proj, dense down, LM head + argmax), dense gate|up + SiLU
 //   fx_moe.h   router, expert gate|up + SiLU, expert down + combine, argmax reduce
 //   fx_mla.h   MLA prep (norm, RoPE, cache append, W_uk absorb), split-KV attend, LSE merge + W_uv
+//   fx_attn.h  split-KV attend on the matrix cores (FX_F_MFMA)
 #pragma once
-#include "fx_mla.h"
+#include "fx_attn.h"
 #include "fx_moe.h"
 
 // kFp8: the kernel variant whose expert stages read FP8 weights (a plan's expert stages are all
@@ -20,7 +21,10 @@ __device__ __forceinline__ void run_stage(const fx_stage& s, FxEnv& env) {
       op_gemv(s, env);
       break;
     case FX_OP_MLA_PREP: op_mla_prep(s, env); break;
-    case FX_OP_MLA_ATTEND: op_mla_attend(s, env); break;
+    case FX_OP_MLA_ATTEND:
+      if (s.flags & FX_F_MFMA) op_mla_attend_mfma(s, env);
+      else op_mla_attend(s, env);
+      break;
     case FX_OP_MLA_MERGE_UV: op_mla_merge_uv(s, env); break;
     case FX_OP_MOE_ROUTER: op_moe_router(s, env); break;
     case FX_OP_MOE_W13: op_moe_w13<kFp8>(s, env); break;

@@ -250,7 +250,8 @@ struct fx_ctx {
   uint64_t* timing = nullptr;
   int timing_cap = 0;
   int last_iters = 0;
-  uint32_t epoch = 0;
+  uint32_t epoch = 1;              // packet tags start above 0, the tag of zeroed packet buffers
+  int64_t next_step = -1;          // step0 + iters of the last launch of the loaded plan (-1: none)
   fx_stage* d_stages = nullptr;
   int n_stages = 0;
   fx_stage* d_epi = nullptr;
@@ -384,6 +385,8 @@ static int check_stage(fx_ctx* c, const fx_stage& s, int idx, int n_total) {
   auto bad = [&](const std::string& m) { return fail(c, FX_E_ARG, "stage " + std::to_string(idx) + ": " + m); };
   for (int k = 0; k < 4; ++k)
     if (s.src[k] < -n_total || s.src[k] >= n_total) return bad("packet source out of range");
+  if ((s.flags & FX_F_MFMA) && s.op != FX_OP_MLA_ATTEND && s.op != FX_OP_MLA_MERGE_UV)
+    return bad("FX_F_MFMA marks the attention and its merge only");
   if (s.flags & FX_F_FP8) {
     const bool head = s.op == FX_OP_GEMV && (s.flags & FX_F_ARGMAX) && s.in_kind == FX_IN_VEC;
     if (s.op != FX_OP_MOE_W13 && s.op != FX_OP_MOE_W2 && !head)
@@ -495,6 +498,7 @@ int fx_load_plan(fx_ctx* c, const fx_stage* st, int32_t n, const fx_stage* epi, 
   c->n_stages = n;
   c->n_epi = n_epi;
   c->fp8 = n_fp8 > 0;
+  c->next_step = -1;
   c->h_stages.assign(st, st + n);
   c->h_epi.assign(epi ? epi : st, epi ? epi + n_epi : st);
   return FX_OK;
@@ -504,6 +508,13 @@ int fx_launch(fx_ctx* c, int32_t iters, int32_t step0, int32_t n_prompt, int64_t
   if (!c) return FX_E_ARG;
   if (!c->d_stages) return fail(c, FX_E_STATE, "no plan loaded");
   if (iters <= 0 || iters > FX_MAX_ITERS || step0 < 0 || !tokens) return fail(c, FX_E_ARG, "iters/step0/tokens");
+  if (n_prompt < 1) return fail(c, FX_E_ARG, "n_prompt must be at least 1");
+  // past the prompt, an iteration's token is the previous iteration's argmax: a launch may start
+  // there only where the previous launch of this plan ended
+  if (step0 >= n_prompt && step0 != c->next_step)
+    return fail(c, FX_E_ARG, "a launch starting at step " + std::to_string(step0) + " (past the prompt of " +
+                                 std::to_string(n_prompt) + ") must continue the previous launch, which ended at " +
+                                 std::to_string(c->next_step));
   for (const fx_stage& s : c->h_stages) {
     if (s.s_max > 0 && step0 + iters > s.s_max) return fail(c, FX_E_ARG, "steps exceed the cache length s_max");
   }
@@ -547,6 +558,7 @@ int fx_launch(fx_ctx* c, int32_t iters, int32_t step0, int32_t n_prompt, int64_t
   HIPCHK(c, hipEventRecord(c->ev1, s));
   c->epoch += (uint32_t)total;
   c->last_iters = iters;
+  c->next_step = (int64_t)step0 + iters;
   return FX_OK;
 }
 

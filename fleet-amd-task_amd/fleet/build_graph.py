@@ -131,11 +131,15 @@ def compile_stages(plan, host):
                         scale=a["softmax_scale"], x=B(a["ql_nope"]), out=B(a["partials"]),
                         aux={0: B(a["c_kv"]), 1: B(a["k_pe"]), 2: B(a["q_pe"]), 5: B(a["crow"]), 6: B(a["done"])},
                         **common)
+            if plan.attn == "mfma":
+                st.flags |= R.FX_F_MFMA
             ins = [(0, a["ql_nope"])]
         elif m == "mla_merge_uv_layer":
             st = _stage(op=R.FX_OP_MLA_MERGE_UV, n_rows=d.NH, d_c=d.D_C, d_r=d.D_R, d_n=d.D_V, split=a["split"],
                         n_splits=a["n_splits"], prow=G.partials_row(d.D_C), x=B(a["input"]), w=B(a["w_uv"]),
                         out=B(a["output"]), aux={4: B(a.get("o_merged")), 6: B(a["done"])}, **common)
+            if plan.attn == "mfma":
+                st.flags |= R.FX_F_MFMA
             ins = [(0, a["done"])]
         elif m == "gang_linear_silu_layer":
             st = _stage(op=R.FX_OP_DENSE_GU, n_rows=d.I_DENSE, k=d.H, x=B(a["input"]), w_norm=B(a["w_norm"]),
@@ -324,7 +328,7 @@ def build(rt, packed, capture, meta, dims: Dims = REAL_DIMS, s_max=1056, layers=
 
 def plan_json(plan):
     return {"dims": plan.dims.__dict__, "s_max": plan.s_max, "layers": plan.layers, "head": plan.head,
-            "split": plan.split, "n_splits": plan.n_splits, "fp8_experts": plan.fp8_experts,
+            "split": plan.split, "n_splits": plan.n_splits, "attn": plan.attn, "fp8_experts": plan.fp8_experts,
             "fp8_head": plan.fp8_head,
             "calls": [{"method": c.method, "label": c.label, "tasks": c.tasks,
                        "args": {k: v for k, v in c.args.items() if isinstance(v, (str, int, float, bool)) or v is None}}

@@ -7,8 +7,9 @@ head.lm_head, head.argmax_reduce, prologue.embed) so --stop-after, the boundary 
 keep their keys. What changes is how calls hand data to each other: instead of the mirage event
 chain, every activation that crosses workgroups is a packet tensor (dtype pk16: bf16 values, two
 per 8-byte packet with the producer's tag; pk32: one f32 per packet), and each consumer waits on
-exactly the packets it reads. Attention runs per XCD (XCD x owns heads 2x, 2x+1), the MoE gate|up
-per slot (slot x on XCD x), everything else over all 256 workers. The residual stream alternates
+exactly the packets it reads. The attention runs split by positions over all workers, every head
+per split (attn="mfma"), or per XCD with heads 2x, 2x+1 on XCD x (attn="valu"); everything else
+runs over all 256 workers. The residual stream alternates
 between two packet vectors, x_res (layer input) and x_mid (after attention).
 """
 import struct
@@ -85,6 +86,7 @@ class Plan:
     calls: list = field(default_factory=list)
     fp8_experts: bool = False   # W13 / W2 are FP8 (codes + per-row scales, pack_weights.quantize_experts)
     fp8_head: bool = False      # W_lm is FP8 too (pack_weights.quantize_head; needs fp8_experts)
+    attn: str = "mfma"          # attention kernel: "mfma" (matrix cores, splits over all workers) or "valu"
 
     def t(self, name, shape, dtype="bf16", kind="new", source=""):
         assert name not in self.tensors, name
@@ -145,21 +147,33 @@ def splits_for(s_max, split=SPLIT, n_splits=None):
     return split, n_splits
 
 
-def default_splits(s_max):
-    """(split, n_splits) of the decode plan: the fewest 32-position tiles per split that keep every
-    split on its own worker of an XCD (at most 32 splits), so the attention runs in one round and the
-    merge reads at most 32 partials per head."""
-    return splits_for(s_max, n_splits=XWORKERS)
+def default_splits(s_max, attn="mfma"):
+    """(split, n_splits) of the decode plan.
+    valu: the fewest 32-position tiles per split that keep every split on its own worker of an XCD
+    (at most 32 splits), so the attention runs in one round and the merge reads at most 32 partials
+    per head.
+    mfma: one split per worker and every head per split, so the splits are short: 32 positions up
+    to 32 splits, then as many positions as keep the split count at most 64 (the merge reads every
+    live split's partial for its head)."""
+    if attn == "valu":
+        return splits_for(s_max, n_splits=XWORKERS)
+    if -(-s_max // SPLIT) <= 32:
+        return splits_for(s_max, SPLIT)
+    return splits_for(s_max, n_splits=64)
 
 
 def build_plan(dims: Dims = REAL_DIMS, s_max: int = 1056, layers: int = 27, head: bool = True, split: int = None,
                n_splits: int = None, iters_cap: int = 32, softmax_scale: float = SOFTMAX_SCALE,
-               eps: float = RMS_EPS, fp8_experts: bool = False, fp8_head: bool = False) -> Plan:
-    """split / n_splits: the attention split (positions) or split count; neither: default_splits."""
+               eps: float = RMS_EPS, fp8_experts: bool = False, fp8_head: bool = False, attn: str = "mfma") -> Plan:
+    """split / n_splits: the attention split (positions) or split count; neither: default_splits.
+    attn: "mfma" (the matrix-core attention: splits over all workers, every head per split) or
+    "valu" (heads over XCDs, score chains on the vector ALUs)."""
     d = dims
     assert 1 <= layers <= d.L
-    split, n_splits = splits_for(s_max, split, n_splits) if (split or n_splits) else default_splits(s_max)
+    assert attn in ("mfma", "valu"), attn
+    split, n_splits = splits_for(s_max, split, n_splits) if (split or n_splits) else default_splits(s_max, attn)
     p = Plan(d, s_max, layers, head, split, n_splits)
+    p.attn = attn
     p.scale = softmax_scale
     p.eps = eps
     p.fp8_experts = fp8_experts

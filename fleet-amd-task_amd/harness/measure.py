@@ -93,7 +93,9 @@ def main():
     ap.add_argument("--seed", type=int, default=20261201)
     ap.add_argument("--out", default=None)
     ap.add_argument("--json", default=None)
-    ap.add_argument("--n-splits", type=int, default=None, help="attention splits (default: 32-position splits)")
+    ap.add_argument("--n-splits", type=int, default=None, help="attention split count (default: the plan's own)")
+    ap.add_argument("--split", type=int, default=None, help="attention split length (a multiple of 32)")
+    ap.add_argument("--attn", choices=("mfma", "valu"), default="mfma", help="attention kernel")
     ap.add_argument("--fp8-experts", action="store_true", help="FP8 expert weights (pack_weights.quantize_experts)")
     args = ap.parse_args()
     d = P.REAL_DIMS
@@ -106,7 +108,7 @@ def main():
         global EXPERT_BYTES
         EXPERT_BYTES = 1
     prompt = P.prompt_ids(args.seed, ctx, d.V)
-    kw = dict(n_splits=args.n_splits, fp8_experts=args.fp8_experts)
+    kw = dict(split=args.split, n_splits=args.n_splits, fp8_experts=args.fp8_experts, attn=args.attn)
     plan = G.build_plan(d, s_max, args.layers, True, **kw)
     runner = B.build(rt, bufs, B.make_capture(rt, plan), B.make_meta(rt, s_max, prompt), d, s_max, args.layers, True,
                      **kw)
@@ -119,6 +121,8 @@ def main():
         Path(args.out).write_text(text + "\n")
     if args.json:
         Path(args.json).write_text(json.dumps(rows) + "\n")
+    del runner, bufs
+    rt.close()
 
 
 if __name__ == "__main__":

@@ -63,7 +63,9 @@ def build_parser():
     ap.add_argument("--ctx", type=int, default=N_PROMPT, help="seeded prompt length when --prompt is not given")
     ap.add_argument("--seed", type=int, default=SEED, help="weight and prompt seed")
     ap.add_argument("--split", type=int, default=None, help="attention split length (a multiple of 32)")
-    ap.add_argument("--n-splits", type=int, default=None, help="attention split count (default: at most 32)")
+    ap.add_argument("--n-splits", type=int, default=None, help="attention split count (default: the plan's own)")
+    ap.add_argument("--attn", choices=("mfma", "valu"), default="mfma",
+                    help="attention kernel: matrix cores over all workers (mfma) or vector-ALU chains per XCD (valu)")
     ap.add_argument("--out", default=None, help="run directory (default: harness/fleet_out/<name>)")
     ap.add_argument("--event-timing", action="store_true", help="per-stage stamps of the last iteration")
     ap.add_argument("--prefill", choices=("decode", "batched"), default="decode",
@@ -125,7 +127,7 @@ def run(args, rt=None):
             packed = P.fill_seeded(rt, d, args.seed, layers=layers, head=args.head)
         t_pack = time.time() - t0
         t1 = time.time()
-        plan_kw = {}
+        plan_kw = {"attn": args.attn}
         if mcfg is not None:
             plan_kw.update(softmax_scale=mcfg.scale, eps=mcfg.eps)
         if args.split:

@@ -113,6 +113,10 @@ enum fx_op {
 #define FX_F_ROUTER 128u   /* MOE_W13 computes the router itself (W_gate in res) */
 #define FX_F_FP8 256u      /* MOE_W13 / MOE_W2, or the LM head GEMV (FX_F_ARGMAX) of a plan whose expert stages
                             * are FP8: w is FP8 (OCP e4m3fn codes [rows][k], then one f32 scale per row) */
+#define FX_F_MFMA 512u     /* MLA_ATTEND / MLA_MERGE_UV: the matrix-core attention. Split j runs on worker
+                            * j % 256 for all heads (tiles of 32 positions; scores and value products on
+                            * v_mfma_f32_16x16x32_bf16); done(aux6) holds one packet per worker, the merge
+                            * waits for workers 0 .. min(live splits, 256) - 1 */
 
 /* One entry of the task table: one operator of the plan (fleet/graph_plan.py Call). */
 typedef struct fx_stage {
@@ -161,7 +165,10 @@ int fx_load_plan(fx_ctx* ctx, const fx_stage* stages, int32_t n_stages, const fx
 /* Replaces mpk() (harness/run_fleet.py:590-593): one persistent launch that runs `iters` decode
  * iterations at positions step0 .. step0 + iters - 1. tokens (int64 [>= step0 + iters + 1]) holds the
  * prompt in [0, n_prompt); iteration i reads tokens[step0 + i] and, when step0 + i + 1 >= n_prompt,
- * the head's argmax is stored to tokens[step0 + i + 1]. stream: a hipStream_t or NULL. */
+ * the head's argmax is stored to tokens[step0 + i + 1]. stream: a hipStream_t or NULL. n_prompt >= 1.
+ * A launch whose step0 lies past the prompt (step0 >= n_prompt) reads its first token from the previous
+ * iteration's argmax, so it must continue the previous launch of the same plan (step0 == that launch's
+ * step0 + iters); any other such launch fails with FX_E_ARG. */
 int fx_run(fx_ctx* ctx, int32_t iters, int32_t step0, int32_t n_prompt, int64_t* tokens, void* stream);
 
 /* fx_run in two halves, so that launches can be queued back to back: fx_launch enqueues the

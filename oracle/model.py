@@ -46,6 +46,15 @@ class Cfg:
         return self.NH * (self.D_N + self.D_R)
 
 
+def cfg_for_plan(plan):
+    """The oracle configuration of a decode plan (fleet.graph_plan.Plan): its dims, eps, softmax
+    scale, attention splits and attention arithmetic."""
+    d = plan.dims
+    return Cfg(H=d.H, NH=d.NH, D_N=d.D_N, D_R=d.D_R, D_V=d.D_V, D_C=d.D_C, V=d.V, L=d.L, I_DENSE=d.I_DENSE,
+               I_MOE=d.I_MOE, E=d.E, TOPK=d.TOPK, N_SHARED=d.N_SHARED, eps=plan.eps, scale=plan.scale,
+               split=plan.split, n_splits=plan.n_splits, attn=getattr(plan, "attn", "valu"))
+
+
 def _expert(W, key, e):
     if hasattr(W, "expert"):
         return W.expert(key, e)

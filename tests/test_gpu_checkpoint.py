@@ -10,6 +10,7 @@ non-trivial pattern, and config.json carries the model's YaRN rope_scaling. Then
     finds the ids, the route log and every boundary equal to the oracle's on the same weights,
     tables and scale.
 """
+import dataclasses
 import json
 import sys
 from pathlib import Path
@@ -101,9 +102,7 @@ def test_checkpoint_load_and_decode(rt, tmp_path):
     assert meta["completed"] and meta["softmax_scale"] == mcfg.scale
     s_max = ctx + iters
     plan = G.build_plan(d, s_max, layers, True, softmax_scale=mcfg.scale, eps=mcfg.eps)
-    cfg = M.Cfg(H=d.H, NH=d.NH, D_N=d.D_N, D_R=d.D_R, D_V=d.D_V, D_C=d.D_C, V=d.V, L=d.L, I_DENSE=d.I_DENSE,
-                I_MOE=d.I_MOE, E=d.E, TOPK=d.TOPK, N_SHARED=d.N_SHARED, eps=mcfg.eps, scale=mcfg.scale,
-                split=plan.split, n_splits=plan.n_splits)
+    cfg = dataclasses.replace(M.cfg_for_plan(plan), eps=mcfg.eps, scale=mcfg.scale)
     cos, sin = mcfg.tables(s_max)
     W = GpuWeights(loaded)
     prompt = P.prompt_ids(SEED, ctx, d.V)

@@ -75,9 +75,7 @@ def test_fp8_model_decode_matches_oracle(rt, fp8_head):
     got = runner.host["tokens"].download()[ctx:ctx + iters].tolist()
     rl = runner.host["route_log"].download()
     x_gpu = runner.x_res()
-    cfg = M.Cfg(H=d.H, NH=d.NH, D_N=d.D_N, D_R=d.D_R, D_V=d.D_V, D_C=d.D_C, V=d.V, L=d.L, I_DENSE=d.I_DENSE,
-                I_MOE=d.I_MOE, E=d.E, TOPK=d.TOPK, N_SHARED=d.N_SHARED, eps=plan.eps, scale=plan.scale,
-                split=plan.split, n_splits=plan.n_splits)
+    cfg = M.cfg_for_plan(plan)
     cos, sin = M.rope_tables(s_max)
     W = GpuWeights(bufs)
     assert W.fp8_experts and W.fp8_head == fp8_head

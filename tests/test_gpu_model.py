@@ -3,8 +3,9 @@
 latent-cache row the run wrote, the final hidden state and the last step's intermediate buffers,
 all bit for bit.
 
-The full 27-layer model at ctx 1,024 is in test_gpu_full_model.py; here the
-real dims with fewer layers keep the oracle in seconds."""
+The full 27-layer model at BASELINE configs 3 and 4 is in test_gpu_full_model.py; here the real
+dims with fewer layers keep the oracle in seconds. Both attention kernels (matrix-core "mfma", the
+default, and vector-ALU "valu") run every case."""
 import numpy as np
 import pytest
 
@@ -19,29 +20,28 @@ pytestmark = pytest.mark.gpu
 
 
 def oracle_cfg(plan, layers):
-    d = plan.dims
-    return M.Cfg(H=d.H, NH=d.NH, D_N=d.D_N, D_R=d.D_R, D_V=d.D_V, D_C=d.D_C, V=d.V, L=d.L, I_DENSE=d.I_DENSE,
-                 I_MOE=d.I_MOE, E=d.E, TOPK=d.TOPK, N_SHARED=d.N_SHARED, eps=plan.eps, scale=plan.scale,
-                 split=plan.split, n_splits=plan.n_splits)
+    return M.cfg_for_plan(plan)
 
 
-def _run_model(rt, layers, n_prompt, n_new, s_max, seed=SEED):
+def _run_model(rt, layers, n_prompt, n_new, s_max, attn, seed=SEED):
     d = P.REAL_DIMS
     bufs = P.fill_seeded(rt, d, seed, layers=layers, head=True)
     prompt = P.prompt_ids(seed, n_prompt, d.V)
-    plan = G.build_plan(d, s_max, layers, True)
+    plan = G.build_plan(d, s_max, layers, True, attn=attn)
     meta = B.make_meta(rt, s_max, prompt)
     cap = B.make_capture(rt, plan)
-    runner = B.build(rt, bufs, cap, meta, d, s_max, layers, True)
-    print(f"[model] layers={layers} n_prompt={n_prompt} n_new={n_new} stages={len(runner.stages)}", flush=True)
+    runner = B.build(rt, bufs, cap, meta, d, s_max, layers, True, attn=attn)
+    print(f"[model] attn={attn} layers={layers} n_prompt={n_prompt} n_new={n_new} stages={len(runner.stages)}",
+          flush=True)
     runner.run(n_prompt - 1 + n_new, 0, n_prompt)
     return d, bufs, prompt, plan, runner, cap
 
 
+@pytest.mark.parametrize("attn", ["mfma", "valu"])
 @pytest.mark.parametrize("layers,n_prompt,n_new", [(2, 40, 4), (3, 70, 3)])
-def test_decode_matches_oracle(rt, layers, n_prompt, n_new):
+def test_decode_matches_oracle(rt, layers, n_prompt, n_new, attn):
     s_max = 96
-    d, bufs, prompt, plan, runner, cap = _run_model(rt, layers, n_prompt, n_new, s_max)
+    d, bufs, prompt, plan, runner, cap = _run_model(rt, layers, n_prompt, n_new, s_max, attn)
     W = GpuWeights(bufs)
     cfg = oracle_cfg(plan, layers)
     cos, sin = M.rope_tables(s_max)
@@ -65,7 +65,8 @@ def test_decode_matches_oracle(rt, layers, n_prompt, n_new):
                 assert rl[i, j].tolist() == r, (i, j, rl[i, j].tolist(), r)
 
 
-def test_last_step_buffers_match_oracle(rt):
+@pytest.mark.parametrize("attn", ["mfma", "valu"])
+def test_last_step_buffers_match_oracle(rt, attn):
     """One decode iteration of a 2-layer model from a seeded random cache (BASELINE config 0's
     setting: 1,024 cached positions ~N(0,1)); every workspace the last layer leaves behind is
     compared (qkva, ql_nope, q_pe, partials, merged o, attn, router logits, top-k, act8, out8,
@@ -73,7 +74,7 @@ def test_last_step_buffers_match_oracle(rt):
     d = P.REAL_DIMS
     layers, s_max, step = 2, 1056, 1024
     bufs = P.fill_seeded(rt, d, SEED, layers=layers, head=True)
-    plan = G.build_plan(d, s_max, layers, True)
+    plan = G.build_plan(d, s_max, layers, True, attn=attn)
     cache = {"c_kv": [], "k_pe": []}
     for l in range(layers):
         cache["c_kv"].append(O.gen_normal_bf16(SEED, P.fnv1a32(f"cache.c_kv.{l}"), step * d.D_C, 1.0).reshape(step, d.D_C))
@@ -83,7 +84,7 @@ def test_last_step_buffers_match_oracle(rt):
     tokens[step] = token
     meta = B.make_meta(rt, s_max, tokens)
     cap = B.make_capture(rt, plan, cache)
-    runner = B.build(rt, bufs, cap, meta, d, s_max, layers, True)
+    runner = B.build(rt, bufs, cap, meta, d, s_max, layers, True, attn=attn)
     runner.run(1, step, step + 1)
     W = GpuWeights(bufs)
     cfg = oracle_cfg(plan, layers)

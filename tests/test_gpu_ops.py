@@ -182,11 +182,20 @@ def test_mla_prep(rt):
     assert mismatch(crow.download(tag=TOUT), np.tile(row, (8, 1))) == 0
 
 
-@pytest.mark.parametrize("s_max,step,split", [(1056, 1023, 32), (1056, 1040, 32), (1056, 1024, 64), (4096, 4095, 128),
-                                              (300, 40, 32), (64, 0, 32), (32768, 32767, 1024),
-                                              (16416, 16383, 160)])
-def test_mla_attend_merge_uv(rt, s_max, step, split):
-    print(f"[attend] s_max={s_max} step={step} split={split}", flush=True)
+ATTEND_POINTS = [(1056, 1023, 32), (1056, 1040, 32), (1056, 1024, 64), (4096, 4095, 128), (300, 40, 32), (64, 0, 32),
+                 (32768, 32767, 1024), (16416, 16383, 160),
+                 (8192, 4127, 32)]                  # 129 live splits: the merge's lse beyond 128 splits
+MFMA_POINTS = [(16416, 16383, 128),                 # exactly 128 live splits
+               (16416, 16384, 128),                 # its next token: 129
+               (8192, 8191, 32),                    # 256 live splits, one per worker
+               (8448, 8447, 32)]                    # 264: workers 0..7 run two splits
+
+
+@pytest.mark.parametrize("attn,s_max,step,split", [("valu",) + p for p in ATTEND_POINTS] +
+                         [("mfma",) + p for p in ATTEND_POINTS + MFMA_POINTS])
+def test_mla_attend_merge_uv(rt, attn, s_max, step, split):
+    print(f"[attend] attn={attn} s_max={s_max} step={step} split={split}", flush=True)
+    mfma = attn == "mfma"
     rng = np.random.default_rng(s_max + step)
     n_splits = -(-s_max // split)
     live = -(-(step + 1) // split)
@@ -201,22 +210,37 @@ def test_mla_attend_merge_uv(rt, s_max, step, split):
     crow = pk(rt, np.tile(np.concatenate([ck[step], kp[step]]), (8, 1)))
     part = sentinel(rt, (n_splits, NH, prow), "f32")
     done = pk_out(rt, (8, 32), "pk32")
-    st = R.FxStage().set(op=R.FX_OP_MLA_ATTEND, n_rows=NH, d_c=DC, d_r=DR, d_n=DN, split=split, n_splits=n_splits,
-                         prow=prow, s_max=s_max, scale=scale, x=pk(rt, ql).ptr, out=part.ptr,
+    flags = R.FX_F_MFMA if mfma else 0
+    st = R.FxStage().set(op=R.FX_OP_MLA_ATTEND, flags=flags, n_rows=NH, d_c=DC, d_r=DR, d_n=DN, split=split,
+                         n_splits=n_splits, prow=prow, s_max=s_max, scale=scale, x=pk(rt, ql).ptr, out=part.ptr,
                          aux={0: dev(rt, ckd, "bf16").ptr, 1: dev(rt, kpd, "bf16").ptr, 2: pk(rt, qp).ptr,
                               5: crow.ptr, 6: done.ptr}, src=[SRC, 0, 0, 0])
     rt.run_stage(st, step=step, tbase=TB, sidx=SIDX)
-    exp = O.mla_attend(ql, qp, ck, kp, step, scale, split=split, n_splits=n_splits)
+    attend = O.mla_attend_mfma if mfma else O.mla_attend
+    exp = attend(ql, qp, ck, kp, step, scale, split=split, n_splits=n_splits)
     got = part.download()
-    assert mismatch(got[:live, :, :DC + 1], exp[:live, :, :DC + 1]) == 0
-    counts = done.download(tag=TOUT).view(np.uint32).reshape(8, 32)
-    assert (counts.sum(axis=1) == live).all()
+    bad = mismatch(got[:live, :, :DC + 1], exp[:live, :, :DC + 1])
+    if bad:
+        d = np.argwhere(got[:live, :, :DC + 1].view(np.uint32) != exp[:live, :, :DC + 1].view(np.uint32))
+        print(f"[attend] {bad} partials differ, first (split, head, col) {d[:6].tolist()}", flush=True)
+    assert bad == 0
+    if mfma:
+        # one done packet per worker that owned a live split (split j on worker j % 256)
+        nown = min(live, 256)
+        words = done.download_raw()
+        vals, tags = R.unpack_packets(words, "pk32")
+        assert (tags[:nown] == TOUT).all() and (tags[nown:] == 0).all()
+        assert int(vals[:nown].view(np.uint32).sum()) == live
+    else:
+        counts = done.download(tag=TOUT).view(np.uint32).reshape(8, 32)
+        assert (counts.sum(axis=1) == live).all()
     # merge + W_uv: inputs tagged TOUT (src = SIDX with the same tbase), outputs TB + SIDX + 2
     W_uv = rng_bf16(rng, (NH, DN, DC), 0.05)
     e_attn, e_obf = O.mla_merge_uv(exp, W_uv, step, split=split)
     attn = pk_out(rt, (NH * DN,))
     om = sentinel(rt, (NH, DC), "bf16")
-    st = R.FxStage().set(op=R.FX_OP_MLA_MERGE_UV, n_rows=NH, d_c=DC, d_r=DR, d_n=DN, split=split, n_splits=n_splits,
+    st = R.FxStage().set(op=R.FX_OP_MLA_MERGE_UV, flags=flags, n_rows=NH, d_c=DC, d_r=DR, d_n=DN, split=split,
+                         n_splits=n_splits,
                          prow=prow, x=part.ptr, w=dev(rt, W_uv, "bf16").ptr, out=attn.ptr,
                          aux={4: om.ptr, 6: done.ptr}, src=[SIDX, 0, 0, 0])
     rt.run_stage(st, step=step, tbase=TB, sidx=SIDX + 1)

@@ -70,9 +70,7 @@ def _setup(rt, layers, ctx, iters):
     meta = B.make_meta(rt, s_max, prompt)
     cap = B.make_capture(rt, plan)
     runner = B.build(rt, packed, cap, meta, d, s_max, layers, True)
-    cfg = M.Cfg(H=d.H, NH=d.NH, D_N=d.D_N, D_R=d.D_R, D_V=d.D_V, D_C=d.D_C, V=d.V, L=d.L, I_DENSE=d.I_DENSE,
-                I_MOE=d.I_MOE, E=d.E, TOPK=d.TOPK, N_SHARED=d.N_SHARED, eps=plan.eps, scale=plan.scale,
-                split=plan.split, n_splits=plan.n_splits)
+    cfg = M.cfg_for_plan(plan)
     return d, s_max, packed, plan, prompt, runner, cfg
 
 

@@ -35,9 +35,7 @@ def test_run_fleet_then_compare(rt, tmp_path):
     d = P.REAL_DIMS
     s_max = ctx + iters
     plan = G.build_plan(d, s_max, layers, True)
-    cfg = M.Cfg(H=d.H, NH=d.NH, D_N=d.D_N, D_R=d.D_R, D_V=d.D_V, D_C=d.D_C, V=d.V, L=d.L, I_DENSE=d.I_DENSE,
-                I_MOE=d.I_MOE, E=d.E, TOPK=d.TOPK, N_SHARED=d.N_SHARED, eps=plan.eps, scale=plan.scale,
-                split=plan.split, n_splits=plan.n_splits)
+    cfg = M.cfg_for_plan(plan)
     cos, sin = M.rope_tables(s_max)
     W = GpuWeights(P.fill_seeded(rt, d, SEED, layers=layers, head=True))
     prompt = P.prompt_ids(SEED, ctx, d.V)
