@@ -5,8 +5,9 @@
 // layer. Per 32-position tile:
 //   QK^T  S[16 heads][32 positions] = two 16x16 output tiles (waves 0, 1), each 18 chained
 //         v_mfma_f32_16x16x32_bf16 over the 576-wide row (latent columns, then rope columns);
-//         A = Q (bf16, held in VGPRs for the whole split), B = 16 staged cache rows (ds_read_b128);
-//   softmax (wave 0) per head over the tile: max, exp, the two 16-position butterflies, bf16(p);
+//         A = Q, B = 16 staged cache rows (both bf16 in LDS, ds_read_b128);
+//   softmax per head over the tile (four heads per wave): max, exp, the two 16-position
+//         butterflies, bf16(p);
 //   PV    tile_pv[16 heads][512 columns] = 32 16x16 output tiles (8 per wave), one instruction over
 //         the tile's 32 positions each; A = bf16(p), B = the staged value rows read transposed
 //         (ds_read_b64_tr_b16), then acc = acc * alpha + tile_pv on the VALU.
@@ -43,15 +44,18 @@ __device__ __forceinline__ fx_i16x4 lds_tr16(const char* p) {
 // rows t0 .. t0 + nt - 1 of a tile that lie below `step`, into registers (chunk q = tid + 256 k:
 // row q / 72, 16-byte chunk q % 72: latent chunks 0..63, rope chunks 64..71). Row `step` and later
 // rows are never read from the caches (they come from the cache-row packets or are zero).
+// (buffer loads with 32-bit byte offsets: the row index stays below 2^21 for any cache that fits)
 __device__ __forceinline__ void am_issue_rows(u32x4* v, const uint16_t* ckv, const uint16_t* kpe, int t0, int nt,
                                               int step) {
+  const __amdgpu_buffer_rsrc_t rc = rsrc(ckv), rk = rsrc(kpe);
 #pragma unroll
   for (int k = 0; k < AM_LOADS; ++k) {
-    const int q = threadIdx.x + k * FX_THREADS;
+    const int q = fx_tid() + k * FX_THREADS;
     const int r = q / 72, c = q % 72;
     const int rr = t0 + r;
     if (r >= nt || rr >= step) { v[k] = (u32x4){0u, 0u, 0u, 0u}; continue; }
-    v[k] = c < 64 ? ld16(ckv + (size_t)rr * 512 + c * 8) : ld16(kpe + (size_t)rr * 64 + (c - 64) * 8);
+    v[k] = c < 64 ? __builtin_amdgcn_raw_buffer_load_b128(rc, (uint32_t)(rr * 1024 + c * 16), 0, 0)
+                  : __builtin_amdgcn_raw_buffer_load_b128(rk, (uint32_t)(rr * 128 + (c - 64) * 16), 0, 0);
   }
 }
 
@@ -84,40 +88,28 @@ __device__ __forceinline__ void op_mla_attend_mfma(const fx_stage& s, FxEnv& env
   // ---- q of every head: ql_nope (2048 pairs of packets) and q_pe (256 pairs), bf16 into LDS rows
   {
     u32x4 w[8];
-    pk_wait_pairs<8>((const void*)s.x, threadIdx.x, FX_THREADS, 2048, tin, env.err, w);
+    pk_wait_pairs<8>((const void*)s.x, fx_tid(), FX_THREADS, 2048, tin, env.err, w);
 #pragma unroll
     for (int n = 0; n < 8; ++n) {
-      const int p = threadIdx.x + n * FX_THREADS;      // pair p: head p / 128, columns 4 (p % 128) ..
+      const int p = fx_tid() + n * FX_THREADS;      // pair p: head p / 128, columns 4 (p % 128) ..
       u32x2 b;
       b.x = w[n].x;
       b.y = w[n].z;
       *(u32x2*)(lds + AM_Q_OFF + (p >> 7) * AM_ROW + (p & 127) * 8) = b;
     }
     u32x4 e[1];
-    pk_wait_pairs<1>((const void*)s.aux[2], threadIdx.x, 0, 256, tin, env.err, e);
+    pk_wait_pairs<1>((const void*)s.aux[2], fx_tid(), 0, 256, tin, env.err, e);
     u32x2 b;
     b.x = e[0].x;
     b.y = e[0].z;
-    *(u32x2*)(lds + AM_Q_OFF + (threadIdx.x >> 4) * AM_ROW + 1024 + (threadIdx.x & 15) * 8) = b;
+    *(u32x2*)(lds + AM_Q_OFF + (fx_tid() >> 4) * AM_ROW + 1024 + (fx_tid() & 15) * 8) = b;
   }
   prof_mark(env, 1);
-  __syncthreads();
-  // Q fragments of the score chains (waves 0, 1): lane (li, lg) holds Q[li][32 ks + 8 lg .. + 8]
-  fx_bf16x8 qf[AM_KS];
-  if (wave < 2) {
-#pragma unroll
-    for (int ks = 0; ks < AM_KS; ++ks) qf[ks] = lds_b128(lds + AM_Q_OFF + li * AM_ROW + (32 * ks + 8 * lg) * 2);
-  }
   int done = 0;
   for (int j = env.worker; j < n_live; j += FX_WORKERS) {
     const int lo = j * split, hi = split_hi(j);
-    // online-softmax state (wave 0; lane (li, lg) keeps heads lg, lg + 4, lg + 8, lg + 12)
-    float m_run[4], l_run[4];
-#pragma unroll
-    for (int hh = 0; hh < 4; ++hh) {
-      m_run[hh] = -__builtin_inff();
-      l_run[hh] = 0.0f;
-    }
+    // online-softmax state of head lg + 4 * wave (the same on the 16 lanes li of lane group lg)
+    float m_run = -__builtin_inff(), l_run = 0.0f;
     // value accumulators: wave w owns columns 128 w .. 128 w + 127 as 8 16-column tiles; lane (li, lg)
     // holds rows (heads) 4 lg .. 4 lg + 3 of column 16 n + li
     fx_f32x4 acc[8];
@@ -130,17 +122,17 @@ __device__ __forceinline__ void op_mla_attend_mfma(const fx_stage& s, FxEnv& env
       // rows past the tile's end as zeros (their value products must be exactly zero)
 #pragma unroll
       for (int k = 0; k < AM_LOADS; ++k) {
-        const int q = threadIdx.x + k * FX_THREADS;
+        const int q = fx_tid() + k * FX_THREADS;
         const int r = q / 72, c = q % 72;
         if (t0 + r != step) *(u32x4*)(lds + AM_KV_OFF + r * AM_ROW + c * 16) = v[k];
       }
-      if (step >= t0 && step < t0 + nt && threadIdx.x < AM_DK / 4) {
+      if (step >= t0 && step < t0 + nt && fx_tid() < AM_DK / 4) {
         u32x4 w[1];
-        pk_wait_pairs<1>(crow, threadIdx.x, 0, threadIdx.x + 1, tin, env.err, w);
+        pk_wait_pairs<1>(crow, fx_tid(), 0, fx_tid() + 1, tin, env.err, w);
         u32x2 b;
         b.x = w[0].x;
         b.y = w[0].z;
-        *(u32x2*)(lds + AM_KV_OFF + (step - t0) * AM_ROW + threadIdx.x * 8) = b;
+        *(u32x2*)(lds + AM_KV_OFF + (step - t0) * AM_ROW + fx_tid() * 8) = b;
       }
       {
         // request the next tile (this split's, or the worker's next split's first)
@@ -155,41 +147,40 @@ __device__ __forceinline__ void op_mla_attend_mfma(const fx_stage& s, FxEnv& env
       __syncthreads();
       // ---- scores: wave q < 2 computes positions 16 q .. 16 q + 15 for every head
       if (wave < 2) {
+        // A = Q[li][32 ks + 8 lg .. + 8], B = row 16 q + li at the same columns, both from LDS
         fx_f32x4 sc = {0.0f, 0.0f, 0.0f, 0.0f};
+        const char* qr = lds + AM_Q_OFF + li * AM_ROW + 16 * lg;
         const char* kr = lds + AM_KV_OFF + (16 * wave + li) * AM_ROW + 16 * lg;
 #pragma unroll
         for (int ks = 0; ks < AM_KS; ++ks)
-          sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qf[ks], lds_b128(kr + 64 * ks), sc, 0, 0, 0);
+          sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(lds_b128(qr + 64 * ks), lds_b128(kr + 64 * ks), sc, 0, 0, 0);
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) S[(4 * lg + jj) * AM_T + 16 * wave + li] = sc[jj] * scale;
       }
       __syncthreads();
       if (done == 0 && t0 == lo) prof_mark(env, 4);
-      // ---- softmax (wave 0): lane (li, lg), heads lg + 4 hh, positions li and li + 16
-      if (wave == 0) {
-#pragma unroll
-        for (int hh = 0; hh < 4; ++hh) {
-          const int h = lg + 4 * hh;
-          const float s0 = li < nt ? S[h * AM_T + li] : -__builtin_inff();
-          const float s1 = li + 16 < nt ? S[h * AM_T + 16 + li] : -__builtin_inff();
-          float mt = fmaxf(s0, s1);
-          mt = fmaxf(mt, xor_lane<1>(mt));
-          mt = fmaxf(mt, xor_lane<2>(mt));
-          mt = fmaxf(mt, xor_lane<4>(mt));
-          mt = fmaxf(mt, xor_lane<8>(mt));
-          const float m_new = m_run[hh] > mt ? m_run[hh] : mt;
-          const float alpha = exp_s(m_run[hh] - m_new);
-          const float p0 = li < nt ? exp_s(s0 - m_new) : 0.0f;
-          const float p1 = li + 16 < nt ? exp_s(s1 - m_new) : 0.0f;
-          const float u0 = butterfly(p0, 16), u1 = butterfly(p1, 16);
-          const float psum = u0 + u1;
-          l_run[hh] = l_run[hh] * alpha + psum;
-          m_run[hh] = m_new;
-          uint16_t* prow_l = (uint16_t*)(lds + AM_P_OFF + h * AM_P_ROW);
-          prow_l[li] = (uint16_t)f2bf(p0);
-          prow_l[16 + li] = (uint16_t)f2bf(p1);
-          if (li == 0) H[h] = alpha;
-        }
+      // ---- softmax: lane (li, lg) of wave w takes head lg + 4 w, positions li and li + 16
+      {
+        const int h = lg + 4 * wave;
+        const float s0 = li < nt ? S[h * AM_T + li] : -__builtin_inff();
+        const float s1 = li + 16 < nt ? S[h * AM_T + 16 + li] : -__builtin_inff();
+        float mt = fmaxf(s0, s1);
+        mt = fmaxf(mt, xor_lane<1>(mt));
+        mt = fmaxf(mt, xor_lane<2>(mt));
+        mt = fmaxf(mt, xor_lane<4>(mt));
+        mt = fmaxf(mt, xor_lane<8>(mt));
+        const float m_new = m_run > mt ? m_run : mt;
+        const float alpha = exp_s(m_run - m_new);
+        const float p0 = li < nt ? exp_s(s0 - m_new) : 0.0f;
+        const float p1 = li + 16 < nt ? exp_s(s1 - m_new) : 0.0f;
+        const float u0 = butterfly(p0, 16), u1 = butterfly(p1, 16);
+        const float psum = u0 + u1;
+        l_run = l_run * alpha + psum;
+        m_run = m_new;
+        uint16_t* prow_l = (uint16_t*)(lds + AM_P_OFF + h * AM_P_ROW);
+        prow_l[li] = (uint16_t)f2bf(p0);
+        prow_l[16 + li] = (uint16_t)f2bf(p1);
+        if (li == 0) H[h] = alpha;
       }
       __syncthreads();
       if (done == 0 && t0 == lo) prof_mark(env, 5);
@@ -220,12 +211,9 @@ __device__ __forceinline__ void op_mla_attend_mfma(const fx_stage& s, FxEnv& env
     }
     // ---- o = acc / l, lse = m + log(l)
     __syncthreads();
-    if (wave == 0 && li == 0) {
-#pragma unroll
-      for (int hh = 0; hh < 4; ++hh) {
-        H[16 + lg + 4 * hh] = m_run[hh];
-        H[32 + lg + 4 * hh] = l_run[hh];
-      }
+    if (li == 0) {
+      H[16 + lg + 4 * wave] = m_run;
+      H[32 + lg + 4 * wave] = l_run;
     }
     __syncthreads();
     {
@@ -238,8 +226,8 @@ __device__ __forceinline__ void op_mla_attend_mfma(const fx_stage& s, FxEnv& env
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) stcf(part, (uint32_t)((j * AM_NH + 4 * lg + jj) * prow + c), acc[n][jj] / linv[jj]);
       }
-      if (threadIdx.x < AM_NH)
-        stcf(part, (uint32_t)((j * AM_NH + threadIdx.x) * prow + 512), H[16 + threadIdx.x] + log_s(H[32 + threadIdx.x]));
+      if (fx_tid() < AM_NH)
+        stcf(part, (uint32_t)((j * AM_NH + fx_tid()) * prow + 512), H[16 + fx_tid()] + log_s(H[32 + fx_tid()]));
     }
     ++done;
   }
@@ -247,6 +235,6 @@ __device__ __forceinline__ void op_mla_attend_mfma(const fx_stage& s, FxEnv& env
   wait_mem();
   __syncthreads();
   prof_mark(env, 7);
-  if (threadIdx.x == 0) pk_put((void*)s.aux[6], (uint32_t)env.worker, (uint32_t)done, tag_out(env));
+  if (fx_tid() == 0) pk_put((void*)s.aux[6], (uint32_t)env.worker, (uint32_t)done, tag_out(env));
   prof_mark(env, 2);
 }

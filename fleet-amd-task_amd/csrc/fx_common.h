@@ -30,7 +30,7 @@ __device__ __forceinline__ uint32_t tag_out(const FxEnv& e) { return e.tbase + (
 
 // profile stamp `slot` of the running stage (thread 0 only)
 __device__ __forceinline__ void prof_mark(const FxEnv& e, int slot) {
-  if (e.pst && threadIdx.x == 0) e.pst[slot] = __builtin_amdgcn_s_memrealtime();
+  if (e.pst && fx_tid() == 0) e.pst[slot] = __builtin_amdgcn_s_memrealtime();
 }
 
 // LDS layout (bytes)

@@ -275,8 +275,17 @@ __device__ __forceinline__ uint32_t xcc_id() {
   asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(x));
   return x & 15u;
 }
-__device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
-__device__ __forceinline__ int wave_id() { return threadIdx.x >> 6; }
+// The thread index as a value the compiler cannot hoist out of the persistent kernel's loops: the
+// empty volatile asm makes every use a fresh value, so each per-thread address is computed inside
+// the stage that uses it instead of living in registers (or scratch) across every stage of the
+// iteration. The operators use fx_tid() wherever they would use threadIdx.x.
+__device__ __forceinline__ int fx_tid() {
+  int t = (int)__builtin_amdgcn_workitem_id_x();
+  asm volatile("" : "+v"(t));
+  return t;
+}
+__device__ __forceinline__ int lane_id() { return fx_tid() & 63; }
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(fx_tid() >> 6); }
 
 // ------------------------------------------------------------------------------------------------
 // reductions
@@ -296,18 +305,18 @@ __device__ __forceinline__ float xor_lane(float v) {
   else if constexpr (O == 4) {
     const float up = dpp_mov<0x104>(v);                   // row_shl:4  (lane + 4)
     const float dn = dpp_mov<0x114>(v);                   // row_shr:4  (lane - 4)
-    return (threadIdx.x & 4) ? dn : up;
+    return (fx_tid() & 4) ? dn : up;
   } else if constexpr (O == 8) return dpp_mov<0x128>(v);  // row_ror:8 (lane ^ 8 inside 16)
   else if constexpr (O == 16) {
     // odd rows of the first operand <-> even rows of the second: [0] = rows (0, 0, 2, 2), [1] = (1, 1, 3, 3)
     const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(unsigned, v), __builtin_bit_cast(unsigned, v),
                                                     false, false);
-    return __builtin_bit_cast(float, (threadIdx.x & 16) ? r[0] : r[1]);
+    return __builtin_bit_cast(float, (fx_tid() & 16) ? r[0] : r[1]);
   } else {
     // upper half of the first operand <-> lower half of the second
     const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, v), __builtin_bit_cast(unsigned, v),
                                                     false, false);
-    return __builtin_bit_cast(float, (threadIdx.x & 32) ? r[0] : r[1]);
+    return __builtin_bit_cast(float, (fx_tid() & 32) ? r[0] : r[1]);
   }
 }
 

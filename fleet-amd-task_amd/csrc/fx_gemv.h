@@ -217,10 +217,10 @@ template <int N>
 __device__ __forceinline__ void poll_row_n(float* xs, const void* src, int K, uint32_t tag, uint32_t* err) {
   u32x4 v[N];
   const int npairs = K >> 2;
-  pk_wait_pairs<N>(src, threadIdx.x, FX_THREADS, npairs, tag, err, v);
+  pk_wait_pairs<N>(src, fx_tid(), FX_THREADS, npairs, tag, err, v);
 #pragma unroll
   for (int n = 0; n < N; ++n) {
-    const int q = threadIdx.x + n * FX_THREADS;
+    const int q = fx_tid() + n * FX_THREADS;
     if (q < npairs) {
       xs[4 * q + 0] = bf_lo(v[n].x);
       xs[4 * q + 1] = bf_hi(v[n].x);
@@ -238,7 +238,7 @@ __device__ __forceinline__ void poll_row(float* xs, const void* src, int K, uint
 
 // plain (non-packet) copy of a bf16 row to a dump buffer
 __device__ __forceinline__ void store_vec_sc1(void* dst, const float* xs, int K) {
-  for (int i = threadIdx.x * 8; i < K; i += FX_THREADS * 8) {
+  for (int i = fx_tid() * 8; i < K; i += FX_THREADS * 8) {
     u32x4 v;
     v.x = pack2(xs[i + 0], xs[i + 1]);
     v.y = pack2(xs[i + 2], xs[i + 3]);
@@ -263,7 +263,7 @@ __device__ __forceinline__ void rmsnorm_body(float* xs, int K, float eps, float*
   }
   __syncthreads();
   const float rs = red[0];
-  for (int i = threadIdx.x * 8; i < K; i += FX_THREADS * 8) {
+  for (int i = fx_tid() * 8; i < K; i += FX_THREADS * 8) {
     float w8[8];
     unpack8(wchunk(i), w8);
 #pragma unroll
@@ -286,7 +286,7 @@ struct NormW {
 __device__ __forceinline__ NormW norm_prefetch(const uint16_t* wn, int K) {
   NormW n;
   n.w = u32x4{0u, 0u, 0u, 0u};
-  if (threadIdx.x * 8 < K) n.w = ld16(wn + threadIdx.x * 8);
+  if (fx_tid() * 8 < K) n.w = ld16(wn + fx_tid() * 8);
   return n;
 }
 __device__ __forceinline__ void rmsnorm_pre(float* xs, const NormW& n, int K, float eps, float* red) {
@@ -375,14 +375,14 @@ __device__ __forceinline__ void op_gemv_w(const fx_stage& s, FxEnv& env, const W
   if (s.in_kind == FX_IN_EMBED) {
     embed_token((const void*)s.aux[3], tag_in(s, env, 1), env);
     const uint16_t* erow = (const uint16_t*)s.aux[0] + (size_t)env.token * K;
-    for (int i = threadIdx.x * 8; i < K; i += FX_THREADS * 8) unpack8(ld16(erow + i), xs + i);
+    for (int i = fx_tid() * 8; i < K; i += FX_THREADS * 8) unpack8(ld16(erow + i), xs + i);
   } else {
     poll_row(xs, (const void*)s.x, K, tag_in(s, env, 0), env.err);
   }
-  if (residual && threadIdx.x < ((r1 - r0 + 3) >> 2)) {
+  if (residual && fx_tid() < ((r1 - r0 + 3) >> 2)) {
     u32x4 v[1];
-    pk_wait_pairs<1>((const void*)s.res, (r0 >> 2) + threadIdx.x, 0, (r1 + 3) >> 2, tag_in(s, env, 2), env.err, v);
-    const int i = 4 * threadIdx.x;
+    pk_wait_pairs<1>((const void*)s.res, (r0 >> 2) + fx_tid(), 0, (r1 + 3) >> 2, tag_in(s, env, 2), env.err, v);
+    const int i = 4 * fx_tid();
     rres[i + 0] = bf_lo(v[0].x);
     rres[i + 1] = bf_hi(v[0].x);
     rres[i + 2] = bf_lo(v[0].z);
@@ -390,7 +390,7 @@ __device__ __forceinline__ void op_gemv_w(const fx_stage& s, FxEnv& env, const W
   }
   if (res_embed) {
     const uint16_t* erow = (const uint16_t*)s.aux[0] + (size_t)env.token * s.n_rows;
-    for (int i = threadIdx.x; i < r1 - r0; i += FX_THREADS) rres[i] = bf2f(erow[r0 + i]);
+    for (int i = fx_tid(); i < r1 - r0; i += FX_THREADS) rres[i] = bf2f(erow[r0 + i]);
   }
   prof_mark(env, 1);
   if (norm) rmsnorm_staged(xs, nw, (const uint16_t*)s.w_norm, K, s.eps, red);
@@ -426,7 +426,7 @@ __device__ __forceinline__ void op_gemv_w(const fx_stage& s, FxEnv& env, const W
     __syncthreads();
     const float* o = rres + FX_MAX_OUT_ROWS / 2;
     const uint32_t tag = tag_out(env);
-    for (int t = threadIdx.x; 4 * t < r1 - r0; t += FX_THREADS)
+    for (int t = fx_tid(); 4 * t < r1 - r0; t += FX_THREADS)
       pk_put2(out, (uint32_t)((r0 >> 1) + 2 * t), pack2(o[4 * t], o[4 * t + 1]), pack2(o[4 * t + 2], o[4 * t + 3]), tag);
   }
   if (want_max) {
@@ -434,7 +434,7 @@ __device__ __forceinline__ void op_gemv_w(const fx_stage& s, FxEnv& env, const W
     int* ri = (int*)(red + 32);
     if (lane_id() == 0) { rv[wave_id()] = best; ri[wave_id()] = best_i; }
     __syncthreads();
-    if (threadIdx.x == 0) {
+    if (fx_tid() == 0) {
       float b = rv[0];
       int bi = ri[0];
       for (int w = 1; w < FX_WAVES; ++w)
@@ -528,7 +528,7 @@ __device__ __forceinline__ void op_dense_gu(const fx_stage& s, FxEnv& env) {
     }
   });
   __syncthreads();
-  if (threadIdx.x < ngroups)
-    pk_put(act, (uint32_t)(q0 + threadIdx.x), pack2(actl[2 * threadIdx.x], actl[2 * threadIdx.x + 1]), tag);
+  if (fx_tid() < ngroups)
+    pk_put(act, (uint32_t)(q0 + fx_tid()), pack2(actl[2 * fx_tid()], actl[2 * fx_tid() + 1]), tag);
   prof_mark(env, 2);
 }

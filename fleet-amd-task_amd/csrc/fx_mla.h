@@ -79,15 +79,15 @@ __device__ __forceinline__ void op_mla_prep(const fx_stage& s, FxEnv& env) {
   const uint16_t* sinr = (const uint16_t*)s.aux[4] + (size_t)env.step * d_r;
   const NormW nw = d_c <= 8 * FX_THREADS ? norm_prefetch((const uint16_t*)s.w_norm, d_c) : NormW{};
   // this thread's RoPE table entries (k_pe and the two q_pe rows), also requested ahead of the input
-  const bool roper = threadIdx.x < d_r * (1 + MLA_HP);
+  const bool roper = fx_tid() < d_r * (1 + MLA_HP);
   float rc = 0.0f, rsn = 0.0f;
   if (roper) {
-    rc = bf2f(cosr[threadIdx.x % d_r]);
-    rsn = bf2f(sinr[threadIdx.x % d_r]);
+    rc = bf2f(cosr[fx_tid() % d_r]);
+    rsn = bf2f(sinr[fx_tid() % d_r]);
   }
   {
     // pairs: latent (q_out .. q_out + d_c) -> 128, k_pe -> 16, q_pe of the two heads -> 2 x 16
-    const int t = threadIdx.x;
+    const int t = fx_tid();
     int q = -1;
     float* dst = nullptr;
     if (t < d_c / 4) { q = (q_out >> 2) + t; dst = xs + 4 * t; }
@@ -109,32 +109,32 @@ __device__ __forceinline__ void op_mla_prep(const fx_stage& s, FxEnv& env) {
   prof_mark(env, 1);
   rmsnorm_staged(xs, nw, (const uint16_t*)s.w_norm, d_c, s.eps, red);
   if (roper) {
-    const int v = threadIdx.x / d_r, i = threadIdx.x % d_r;
-    rp[threadIdx.x] = rope64_cs(kp + 64 * v, rc, rsn, i);
+    const int v = fx_tid() / d_r, i = fx_tid() % d_r;
+    rp[fx_tid()] = rope64_cs(kp + 64 * v, rc, rsn, i);
   }
   __syncthreads();
   if (env.xcd == 0) {
     // the cache row (plain), complete before any packet of this worker is published
     store_vec_sc1((uint8_t*)s.aux[0] + (size_t)env.step * d_c * 2, xs, d_c);
-    if (threadIdx.x < d_r / 8) {
-      const float* r = rp + 8 * threadIdx.x;
+    if (fx_tid() < d_r / 8) {
+      const float* r = rp + 8 * fx_tid();
       u32x4 v;
       v.x = pack2(r[0], r[1]);
       v.y = pack2(r[2], r[3]);
       v.z = pack2(r[4], r[5]);
       v.w = pack2(r[6], r[7]);
-      stc16((uint8_t*)s.aux[1] + (size_t)env.step * d_r * 2, threadIdx.x * 16, v);
+      stc16((uint8_t*)s.aux[1] + (size_t)env.step * d_r * 2, fx_tid() * 16, v);
     }
     wait_mem();
   }
   // crow packets of this XCD: latent (d_c / 2) then k_pe (d_r / 2); q_pe packets of its heads
   void* crow = (uint8_t*)s.aux[5] + (size_t)env.xcd * (d_c + d_r) / 2 * 8;
-  for (int t = threadIdx.x; t < (d_c + d_r) / 4; t += FX_THREADS) {
+  for (int t = fx_tid(); t < (d_c + d_r) / 4; t += FX_THREADS) {
     const float* r = t < d_c / 4 ? xs + 4 * t : rp + 4 * (t - d_c / 4);
     pk_put2(crow, (uint32_t)(2 * t), pack2(r[0], r[1]), pack2(r[2], r[3]), tout);
   }
-  if (threadIdx.x < MLA_HP * d_r / 4) {
-    const int hh = threadIdx.x / (d_r / 4), j = threadIdx.x % (d_r / 4);
+  if (fx_tid() < MLA_HP * d_r / 4) {
+    const int hh = fx_tid() / (d_r / 4), j = fx_tid() % (d_r / 4);
     const float* r = rp + 64 + hh * 64 + 4 * j;
     pk_put2((void*)s.aux[2], (uint32_t)(((h0 + hh) * d_r) / 2 + 2 * j), pack2(r[0], r[1]), pack2(r[2], r[3]), tout);
   }
@@ -165,7 +165,7 @@ __device__ __forceinline__ void att_issue_rows(u32x4* v, const uint16_t* ckv, co
                                                int step, int d_c, int d_r) {
 #pragma unroll
   for (int k = 0; k < ATT_LOADS; ++k) {
-    const int q = threadIdx.x + k * FX_THREADS;
+    const int q = fx_tid() + k * FX_THREADS;
     const int r = q / ATT_CHUNKS, c = q % ATT_CHUNKS;
     int rr = t0 + (r < nt ? r : 0);
     if (rr >= step) rr = t0 < step ? t0 : -1;
@@ -214,7 +214,7 @@ __device__ __forceinline__ void op_mla_attend(const fx_stage& s, FxEnv& env) {
     __syncthreads();
     if (!have_q) {
       // q rows of the XCD's heads: ql 2 x 128 pairs (thread t), qp 2 x 16 pairs (threads 0..31)
-      const int t = threadIdx.x;
+      const int t = fx_tid();
       {
         const int hh = t / (d_c / 4), i = t % (d_c / 4);
         const int q = ((h0 + hh) * d_c >> 2) + i;
@@ -243,14 +243,14 @@ __device__ __forceinline__ void op_mla_attend(const fx_stage& s, FxEnv& env) {
     m_run = -__builtin_inff();
     l_run = 0.0f;
     // accumulators: thread -> head ph = tid >> 7, columns pc .. pc + 3
-    const int ph = threadIdx.x >> 7, pc = (threadIdx.x & 127) * 4;
+    const int ph = fx_tid() >> 7, pc = (fx_tid() & 127) * 4;
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     for (int t0 = lo; t0 < hi; t0 += ATT_PASS) {
       const int nt = pass_rows(t0, hi);
       const int ntA = nt < ATT_T ? nt : ATT_T, ntB = nt - ntA;
 #pragma unroll
       for (int k = 0; k < ATT_LOADS; ++k) {
-        const int q = threadIdx.x + k * FX_THREADS;
+        const int q = fx_tid() + k * FX_THREADS;
         const int r = q / ATT_CHUNKS, c = q % ATT_CHUNKS;
         if (r < nt && t0 + r != step) *(u32x4*)(buf + r * ATT_ROW + c * 8) = v[k];
       }
@@ -260,11 +260,11 @@ __device__ __forceinline__ void op_mla_attend(const fx_stage& s, FxEnv& env) {
         if (nt0 >= hi) { nj = j + env.xworkers; nt0 = nj * split; nhi = nj < n_live ? split_hi(nj) : 0; }
         if (nj < n_live) att_issue_rows(v, ckv, kpe, nt0, pass_rows(nt0, nhi), step, d_c, d_r);
       }
-      if (step >= t0 && step < t0 + nt && threadIdx.x < (d_c + d_r) / 4) {
+      if (step >= t0 && step < t0 + nt && fx_tid() < (d_c + d_r) / 4) {
         // row `step` from the XCD's packet copy of the cache row
         u32x4 w[1];
-        pk_wait_pairs<1>(crow, threadIdx.x, 0, threadIdx.x + 1, tin, env.err, w);
-        uint32_t* dst = (uint32_t*)(buf + (step - t0) * ATT_ROW) + 2 * threadIdx.x;
+        pk_wait_pairs<1>(crow, fx_tid(), 0, fx_tid() + 1, tin, env.err, w);
+        uint32_t* dst = (uint32_t*)(buf + (step - t0) * ATT_ROW) + 2 * fx_tid();
         dst[0] = w[0].x;
         dst[1] = w[0].z;
       }
@@ -274,7 +274,7 @@ __device__ __forceinline__ void op_mla_attend(const fx_stage& s, FxEnv& env) {
       // * scale. Consecutive lanes take consecutive rows (row stride 1168 B: conflict-free b128
       // reads) and share q (broadcast). A missing tile-B row is computed on stale data and dropped.
       {
-        const int h = threadIdx.x >> 7, k = (threadIdx.x >> 5) & 3, t = threadIdx.x & 31;
+        const int h = fx_tid() >> 7, k = (fx_tid() >> 5) & 3, t = fx_tid() & 31;
         float a = 0.0f, a2 = 0.0f, b = 0.0f, b2 = 0.0f;
         const uint16_t* kr = buf + t * ATT_ROW;
         const uint16_t* kr2 = buf + (ATT_T + t) * ATT_ROW;
@@ -371,9 +371,9 @@ __device__ __forceinline__ void op_mla_attend(const fx_stage& s, FxEnv& env) {
       // m_B = max(m_A, max_t s_B), alpha = exp(m_prev - m_new), p = exp(s - m_new); each tile's sum
       // of p runs sequentially in t (lane by lane through scalar reads). The running (m, l) stays on
       // wave 0: l = (l * alpha_A + psum_A) * alpha_B + psum_B, the tile order of the spec.
-      if (threadIdx.x < 64 || (threadIdx.x < 128 && ntB > 0)) {
-        const int tile = threadIdx.x >> 6;
-        const int h = (threadIdx.x >> 5) & 1, t = threadIdx.x & 31;
+      if (fx_tid() < 64 || (fx_tid() < 128 && ntB > 0)) {
+        const int tile = fx_tid() >> 6;
+        const int h = (fx_tid() >> 5) & 1, t = fx_tid() & 31;
         auto tile_score = [&](int tl, int ntt) {
           float sc = -__builtin_inff();
           if (t < ntt) {
@@ -425,9 +425,9 @@ __device__ __forceinline__ void op_mla_attend(const fx_stage& s, FxEnv& env) {
       }
       __syncthreads();
       if (done == 0 && t0 == lo) prof_mark(env, 5);
-      if (threadIdx.x < 64) {
+      if (fx_tid() < 64) {
         // wave 0 folds tile B's sum into l and publishes (m, l) for the split's output
-        const int h = (threadIdx.x >> 5) & 1, t = threadIdx.x & 31;
+        const int h = (fx_tid() >> 5) & 1, t = fx_tid() & 31;
         if (ntB > 0) l_run = l_run * hs[h * 4 + 3] + psB[h];
         if (t == 0) {
           hs[h * 4 + 0] = m_run;
@@ -545,7 +545,7 @@ __device__ __forceinline__ void op_mla_attend(const fx_stage& s, FxEnv& env) {
       o.z = __float_as_uint(acc[2] / l);
       o.w = __float_as_uint(acc[3] / l);
       stc16(part, (base + pc) * 4, o);
-      if ((threadIdx.x & 127) == 0) stcf(part, base + d_c, hs[ph * 4 + 0] + log_s(l));
+      if ((fx_tid() & 127) == 0) stcf(part, base + d_c, hs[ph * 4 + 0] + log_s(l));
     }
     ++done;
   }
@@ -553,7 +553,7 @@ __device__ __forceinline__ void op_mla_attend(const fx_stage& s, FxEnv& env) {
   wait_mem();
   __syncthreads();
   prof_mark(env, 7);
-  if (threadIdx.x == 0)
+  if (fx_tid() == 0)
     pk_put((void*)s.aux[6], (uint32_t)(env.xcd * FX_XWORKERS + env.xrank), (uint32_t)done, tag_out(env));
   prof_mark(env, 2);
 }
@@ -562,7 +562,7 @@ __device__ __forceinline__ void op_mla_attend(const fx_stage& s, FxEnv& env) {
 // 152-165: M = max lse, w_j = exp(lse_j - M), o = (sum_j w_j o_j, sequential fma) / (sum_j w_j,
 // sequential) -> bf16), then attn[h*d_v + v] = bf16(dot(o, W_uv[h][v])) for 8 rows v each
 // (harness/numpy_ref.py:168-174).
-#define MERGE_BATCH 32
+#define MERGE_BATCH 40   // splits whose partials are requested at once (every live split up to ctx 1280)
 __device__ __forceinline__ void op_mla_merge_uv(const fx_stage& s, FxEnv& env) {
   const int nh = s.n_rows, d_c = s.d_c, d_v = s.d_n, prow = s.prow;
   const int hh = env.xrank >> 4;
@@ -600,14 +600,13 @@ __device__ __forceinline__ void op_mla_merge_uv(const fx_stage& s, FxEnv& env) {
     if (lane_id() < live) l0 = ldcf(part, (uint32_t)((lane_id() * nh + h) * prow + d_c));
     if (lane_id() + 64 < live) l1 = ldcf(part, (uint32_t)(((lane_id() + 64) * nh + h) * prow + d_c));
   }
-  // every thread: 2 columns of o; the first 32 splits' values are requested before anything waits
-  const int pc = threadIdx.x * 2;
+  // every thread: 2 columns of o; the first MERGE_BATCH live splits' values are requested before
+  // anything waits (live is uniform: the branches are scalar)
+  const int pc = fx_tid() * 2;
   u32x2 o[MERGE_BATCH];
 #pragma unroll
-  for (int k = 0; k < MERGE_BATCH; ++k) {
-    const int j = k < live ? k : live - 1;
-    o[k] = ldc8(part, (uint32_t)((j * nh + h) * prow + pc) * 4);
-  }
+  for (int k = 0; k < MERGE_BATCH; ++k)
+    if (k < live) o[k] = ldc8(part, (uint32_t)((k * nh + h) * prow + pc) * 4);
   // wave 0: lse_j, M = max lse, w_j = exp(lse_j - M) into LDS, den = sum_j w_j in j order
   if (wave_id() == 0) {
     // the rest of the lse (more than 128 splits) from LDS
@@ -636,10 +635,8 @@ __device__ __forceinline__ void op_mla_merge_uv(const fx_stage& s, FxEnv& env) {
   for (int j0 = 0; j0 < live; j0 += MERGE_BATCH) {
     if (j0 > 0) {
 #pragma unroll
-      for (int k = 0; k < MERGE_BATCH; ++k) {
-        const int j = j0 + k < live ? j0 + k : live - 1;
-        o[k] = ldc8(part, (uint32_t)((j * nh + h) * prow + pc) * 4);
-      }
+      for (int k = 0; k < MERGE_BATCH; ++k)
+        if (j0 + k < live) o[k] = ldc8(part, (uint32_t)(((j0 + k) * nh + h) * prow + pc) * 4);
     }
 #pragma unroll
     for (int k = 0; k < MERGE_BATCH; ++k) {
@@ -663,9 +660,9 @@ __device__ __forceinline__ void op_mla_merge_uv(const fx_stage& s, FxEnv& env) {
       if (row[i] >= 0 && lane_id() == 0) o8[row[i] - v0] = bf16r(acc[i]);
   });
   __syncthreads();
-  if (threadIdx.x < nrows / 4) {
-    const float* r = o8 + 4 * threadIdx.x;
-    pk_put2((void*)s.out, (uint32_t)((h * d_v + v0) / 2 + 2 * threadIdx.x), pack2(r[0], r[1]), pack2(r[2], r[3]),
+  if (fx_tid() < nrows / 4) {
+    const float* r = o8 + 4 * fx_tid();
+    pk_put2((void*)s.out, (uint32_t)((h * d_v + v0) / 2 + 2 * fx_tid()), pack2(r[0], r[1]), pack2(r[2], r[3]),
             tag_out(env));
   }
   prof_mark(env, 2);

@@ -189,9 +189,9 @@ __device__ __forceinline__ void op_moe_w13_t(const fx_stage& s, FxEnv& env, cons
     }
   }
   __syncthreads();
-  if (threadIdx.x < nA) {
-    const int a = a0 + threadIdx.x;
-    pk_put(act, (uint32_t)((topk + a / PG) * half + a % PG), pack2(actl[2 * threadIdx.x], actl[2 * threadIdx.x + 1]),
+  if (fx_tid() < nA) {
+    const int a = a0 + fx_tid();
+    pk_put(act, (uint32_t)((topk + a / PG) * half + a % PG), pack2(actl[2 * fx_tid()], actl[2 * fx_tid() + 1]),
            tag);
   }
   // the routing stays in LDS for the expert-down stage that follows on this worker
@@ -215,10 +215,10 @@ __device__ __forceinline__ void op_moe_w13_t(const fx_stage& s, FxEnv& env, cons
     if (lane_id() == 0) remv[wave_id()] = acc[0];
   }
   __syncthreads();
-  if (threadIdx.x < nB) {
-    const int r = b0 + threadIdx.x;
-    const int i = nA + threadIdx.x;
-    if (threadIdx.x == nB4) {
+  if (fx_tid() < nB) {
+    const int r = b0 + fx_tid();
+    const int i = nA + fx_tid();
+    if (fx_tid() == nB4) {
       // rows gate p, up p, gate p + 1, up p + 1 of the split group: emit's arithmetic
       float a[2];
 #pragma unroll
@@ -290,10 +290,10 @@ __device__ __forceinline__ void op_moe_w2_t(const fx_stage& s, FxEnv& env, const
     tile_load(tr0, W, I, w, rowB);
     tile_load(tr1, W, I, w + FX_WAVES, rowB);
   }
-  if (threadIdx.x < (nrow >> 2)) {
+  if (fx_tid() < (nrow >> 2)) {
     u32x4 v[1];
-    pk_wait_pairs<1>((const void*)s.res, (r0 >> 2) + threadIdx.x, 0, (r0 + nrow) >> 2, tag_in(s, env, 2), env.err, v);
-    const int i = 4 * threadIdx.x;
+    pk_wait_pairs<1>((const void*)s.res, (r0 >> 2) + fx_tid(), 0, (r0 + nrow) >> 2, tag_in(s, env, 2), env.err, v);
+    const int i = 4 * fx_tid();
     rres[i + 0] = bf_lo(v[0].x);
     rres[i + 1] = bf_hi(v[0].x);
     rres[i + 2] = bf_lo(v[0].z);
@@ -342,8 +342,8 @@ __device__ __forceinline__ void op_moe_w2_t(const fx_stage& s, FxEnv& env, const
                 [&](int g, const int* row, const float* acc) { emit(0, g, acc); });
   }
   __syncthreads();
-  if (threadIdx.x < nrow) {
-    const int r = threadIdx.x;
+  if (fx_tid() < nrow) {
+    const int r = fx_tid();
     float acc = rres[r];
     for (int sl = 0; sl < nslots; ++sl) {
       const float t = o8[sl * W2_ROWS + r] * wts[sl];
@@ -354,8 +354,8 @@ __device__ __forceinline__ void op_moe_w2_t(const fx_stage& s, FxEnv& env, const
       for (int sl = 0; sl < nslots; ++sl) stc2((void*)s.aux[1], (uint32_t)(sl * H + r0 + r) * 2, f2bf(o8[sl * W2_ROWS + r]));
   }
   __syncthreads();
-  if (threadIdx.x < (nrow >> 1))
-    pk_put((void*)s.out, (uint32_t)((r0 >> 1) + threadIdx.x), pack2(red[2 * threadIdx.x], red[2 * threadIdx.x + 1]),
+  if (fx_tid() < (nrow >> 1))
+    pk_put((void*)s.out, (uint32_t)((r0 >> 1) + fx_tid()), pack2(red[2 * fx_tid()], red[2 * fx_tid() + 1]),
            tag_out(env));
   prof_mark(env, 2);
 }
