@@ -66,14 +66,6 @@ def thresholds(calibration):
     return th, f"{BD.THRESHOLD_MULTIPLIER:g} x calibrated floor"
 
 
-def _ids_by_weight(key, side):
-    k9 = key.replace(".B10.topk_w", ".B9.topk_idx")
-    if k9 not in side:
-        return None
-    return dict(zip(np.asarray(side[k9]).reshape(-1).astype(np.int64).tolist(),
-                    np.asarray(side[key], np.float64).reshape(-1).tolist()))
-
-
 def _sort_key(key):
     m = re.match(r"^L(\d+)\.B(\d+)\.", key)
     if m:
@@ -82,115 +74,144 @@ def _sort_key(key):
     return (int(m.group(1)), 99, key) if m else (10 ** 6, 0, key)
 
 
+# ---- the verdict rules, as this build states them (the output keys are the reference's, which its
+# reports and users read):
+#  ids         the common prefix of the two id lists is compared; the first differing position, if
+#              any, is the divergence (FAIL); with none, equal lengths PASS and a shorter list PARTIAL.
+#  route log   per (step, MoE layer) the reference's top-k ids against the first k of the Fleet log,
+#              as sets. Without the reference's router weights every difference fails. With them,
+#              differences are judged in (step, layer) order: one expert swapped for another whose
+#              reference weight is within tol_rel of the larger of the two is a tie; any other
+#              difference is a cascade once a tie or cascade has occurred, else a disagreement;
+#              disagreements fail.
+#  boundaries  one row per boundary key of the Fleet dump: layers the reference did not capture are
+#              NOT_CAPTURED; keys from a later iteration are judged against that iteration's
+#              reference dump, NOT_COMPARABLE without one; a key the reference lacks is MISSING_REF;
+#              top-k ids (B9) compare as sets, the token (B16) exactly, top-k weights (B10) matched
+#              by expert id; every other key by rel_err = |fleet - ref|_2 / |ref|_2 against its
+#              class threshold.
+
+
+def _judge_ids(a, b, row):
+    fa = sorted(int(v) for v in np.asarray(a).reshape(-1))
+    fb = sorted(int(v) for v in np.asarray(b).reshape(-1))
+    row.update(result="PASS" if fa == fb else "FAIL", detail=f"fleet {fa} ref {fb}")
+
+
+def _judge_exact(a, b, row):
+    va, vb = (int(np.asarray(x).reshape(-1)[0]) for x in (a, b))
+    row.update(result="PASS" if va == vb else "FAIL", detail=f"fleet {va} ref {vb}")
+
+
+def _judge_tensor(a, b, row, threshold, floor):
+    mt = metrics(a, b)
+    if "shape_mismatch" in mt:
+        row.update(result="FAIL", detail=f"shape mismatch {mt['shape_mismatch']}")
+        return
+    row.update(mt, threshold=threshold, floor=floor)
+    row["result"] = "FAIL" if mt["rel_err"] > threshold else "PASS"
+
+
+def _weights_by_expert(key, dump):
+    """{expert id: weight} of a B10 key through the same layer's B9 ids, or None."""
+    ids_key = key.replace(".B10.topk_w", ".B9.topk_idx")
+    if ids_key not in dump:
+        return None
+    ids = np.asarray(dump[ids_key]).reshape(-1).astype(np.int64)
+    return {int(e): float(w) for e, w in zip(ids, np.asarray(dump[key], np.float64).reshape(-1))}
+
+
 def compare_boundaries(ref, fleet, th, floor=None, iters=1, ref_later=None):
-    """One row per boundary key of the Fleet file (auxiliary tensors skipped)."""
+    """One row per boundary key of the Fleet file (auxiliary tensors skipped), in layer order."""
+    captured = {int(m.group(1)) for m in (re.match(r"^L(\d+)\.", k) for k in ref) if m}
     rows = []
-    ref_layers = sorted({int(k.split(".")[0][1:]) for k in ref if re.match(r"^L\d+\.", k)})
-    for key in sorted(fleet, key=_sort_key):
-        cls = BD.boundary_class(key)
-        if cls is None:
-            continue
-        row = {"key": key, "boundary": BD.boundary_id(key), "class": cls}
+    for key in sorted((k for k in fleet if BD.boundary_class(k) is not None), key=_sort_key):
+        cls, bid = BD.boundary_class(key), BD.boundary_id(key)
+        row = {"key": key, "boundary": bid, "class": cls}
         rows.append(row)
-        m = re.match(r"^L(\d+)\.", key)
-        if m and int(m.group(1)) not in ref_layers:
-            row.update(result="NOT_CAPTURED", detail=f"the reference captures layers {ref_layers}")
+        layer = re.match(r"^L(\d+)\.", key)
+        if layer is not None and int(layer.group(1)) not in captured:
+            row.update(result="NOT_CAPTURED", detail=f"the reference captures layers {sorted(captured)}")
             continue
         it = BD.boundary_iteration(key, iters)
-        side = ref
         if it > 0:
             row["iteration"] = it
-            if ref_later is None:
-                row.update(result="NOT_COMPARABLE",
-                           detail=f"dumped from iteration {it}; the reference has no ref_boundaries_step{it}")
-                continue
-            side = ref_later
+        side = ref if it == 0 else ref_later
+        if side is None:
+            row.update(result="NOT_COMPARABLE",
+                       detail=f"dumped from iteration {it}; the reference has no ref_boundaries_step{it}")
+            continue
         if key not in side:
             row["result"] = "MISSING_REF"
             continue
         a, b = fleet[key], side[key]
-        if row["boundary"] == "B9":
-            fa = sorted(np.asarray(a).reshape(-1).astype(np.int64).tolist())
-            fb = sorted(np.asarray(b).reshape(-1).astype(np.int64).tolist())
-            row.update(result="PASS" if fa == fb else "FAIL", detail=f"fleet {fa} ref {fb}")
-            continue
-        if cls == "exact":
-            va, vb = int(np.asarray(a).reshape(-1)[0]), int(np.asarray(b).reshape(-1)[0])
-            row.update(result="PASS" if va == vb else "FAIL", detail=f"fleet {va} ref {vb}")
-            continue
-        if row["boundary"] == "B10":
-            # the reference's top-k order is unspecified: weights matched by expert id
-            fa, rb = _ids_by_weight(key, fleet), _ids_by_weight(key, side)
-            if fa is not None and rb is not None:
-                if set(fa) != set(rb):
-                    row.update(result="FAIL", detail=f"expert sets differ: fleet {sorted(fa)} ref {sorted(rb)}")
-                    continue
-                a, b = [fa[e] for e in sorted(rb)], [rb[e] for e in sorted(rb)]
-        mt = metrics(a, b)
-        if "shape_mismatch" in mt:
-            row.update(result="FAIL", detail=f"shape mismatch {mt['shape_mismatch']}")
-            continue
-        row.update(mt)
-        row["threshold"] = th[cls]
-        row["floor"] = floor.get(cls) if floor else None
-        row["result"] = "PASS" if mt["rel_err"] <= th[cls] else "FAIL"
+        if bid == "B9":
+            _judge_ids(a, b, row)
+        elif cls == "exact":
+            _judge_exact(a, b, row)
+        else:
+            if bid == "B10":
+                wf, wr = _weights_by_expert(key, fleet), _weights_by_expert(key, side)
+                if wf is not None and wr is not None:
+                    if wf.keys() != wr.keys():
+                        row.update(result="FAIL", detail=f"expert sets differ: fleet {sorted(wf)} ref {sorted(wr)}")
+                        continue
+                    order = sorted(wr)
+                    a, b = [wf[e] for e in order], [wr[e] for e in order]
+            _judge_tensor(a, b, row, th[cls], floor.get(cls) if floor else None)
     return rows
 
 
 def compare_ids(ref_ids, fleet_ids):
     n = min(len(ref_ids), len(fleet_ids))
-    first = next((i for i in range(n) if ref_ids[i] != fleet_ids[i]), None)
-    if first is not None:
-        result = "FAIL"
-    elif len(fleet_ids) == len(ref_ids):
-        result = "PASS"
-    else:
-        result = "PARTIAL"
+    differ = np.asarray(ref_ids[:n], np.int64) != np.asarray(fleet_ids[:n], np.int64)
+    first = int(np.argmax(differ)) if differ.any() else None
+    result = "FAIL" if first is not None else ("PASS" if len(ref_ids) == len(fleet_ids) else "PARTIAL")
     return {"n_ref": len(ref_ids), "n_fleet": len(fleet_ids), "compared": n,
             "matched_prefix": n if first is None else first, "first_divergence": first,
             "all_match": result == "PASS", "result": result}
 
 
+def _route_differences(ref_log, fleet_log):
+    """(step, layer, ref set, fleet set) of every (step, MoE layer) whose top-k sets differ."""
+    for s, (rs, fs) in enumerate(zip(ref_log, fleet_log)):
+        for j, (re_, fe) in enumerate(zip(rs, fs)):
+            r = sorted(re_["idx"])
+            f = sorted(fe["idx"][:len(r)])
+            if r != f:
+                yield s, j, r, f
+
+
 def compare_route_log(ref_log, fleet_log, tol_rel=ROUTE_TOL):
     """tol_rel: ROUTE_TOL, or THRESHOLD_MULTIPLIER x the calibrated router floor."""
-    has_w = bool(ref_log) and all("w_all" in e for step in ref_log for e in step)
-    mismatches, ties, cascades, disagreements = [], [], [], []
-    steps = min(len(ref_log), len(fleet_log))
-    for s in range(steps):
-        for j in range(min(len(ref_log[s]), len(fleet_log[s]))):
-            r = sorted(ref_log[s][j]["idx"])
-            f = sorted(fleet_log[s][j]["idx"][:len(r)])
-            if r == f:
-                continue
-            m = {"step": s, "moe_layer_index": j, "ref": r, "fleet": f}
-            mismatches.append(m)
-            if not has_w:
-                continue
-            left, came = sorted(set(r) - set(f)), sorted(set(f) - set(r))
-            if len(left) == 1 and len(came) == 1:
-                w = ref_log[s][j]["w_all"]
-                wl, wc = float(w[left[0]]), float(w[came[0]])
-                gap, tol = abs(wl - wc), tol_rel * max(wl, wc)
-                m.update(left=left[0], came=came[0], w_left=wl, w_came=wc, gap=gap, tol=tol)
-                if gap <= tol:
-                    m["class"] = "tie"
-                    ties.append(m)
-                    continue
-            if ties or cascades:
-                m["class"] = "cascade"
-                cascades.append(m)
-            else:
-                m["class"] = "disagreement"
-                disagreements.append(m)
-    if steps == 0:
-        result = "SKIP"
-    elif not has_w:
-        result = "PASS" if not mismatches else "FAIL"
+    weighted = bool(ref_log) and all("w_all" in e for step in ref_log for e in step)
+    out = {"steps_compared": min(len(ref_log), len(fleet_log)), "rule": "tie" if weighted else "exact",
+           "tol_rel": tol_rel if weighted else None, "mismatches": [], "ties": [], "cascades": [],
+           "disagreements": []}
+    for s, j, r, f in _route_differences(ref_log, fleet_log):
+        m = {"step": s, "moe_layer_index": j, "ref": r, "fleet": f}
+        out["mismatches"].append(m)
+        if not weighted:
+            continue
+        gone, new = sorted(set(r) - set(f)), sorted(set(f) - set(r))
+        cls = None
+        if len(gone) == len(new) == 1:
+            w = ref_log[s][j]["w_all"]
+            w_gone, w_new = float(w[gone[0]]), float(w[new[0]])
+            m.update(left=gone[0], came=new[0], w_left=w_gone, w_came=w_new, gap=abs(w_gone - w_new),
+                     tol=tol_rel * max(w_gone, w_new))
+            if m["gap"] <= m["tol"]:
+                cls = "tie"
+        if cls is None:
+            cls = "cascade" if (out["ties"] or out["cascades"]) else "disagreement"
+        m["class"] = cls
+        out[{"tie": "ties", "cascade": "cascades", "disagreement": "disagreements"}[cls]].append(m)
+    if out["steps_compared"] == 0:
+        out["result"] = "SKIP"
     else:
-        result = "FAIL" if disagreements else "PASS"
-    return {"steps_compared": steps, "rule": "tie" if has_w else "exact", "tol_rel": tol_rel if has_w else None,
-            "mismatches": mismatches, "ties": ties, "cascades": cascades, "disagreements": disagreements,
-            "result": result}
+        failing = out["disagreements"] if weighted else out["mismatches"]
+        out["result"] = "FAIL" if failing else "PASS"
+    return out
 
 
 def _fmt(x, nd=3):
