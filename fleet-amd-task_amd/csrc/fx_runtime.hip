@@ -240,6 +240,16 @@ __global__ void fx_fill_kernel(uint16_t* dst, uint64_t n, uint16_t v) {
 }
 
 // ------------------------------------------------------------------------------------------------
+// The allocation-free attention entry (fx_mla_attend_merge_noalloc): the split partials and the
+// per-worker done packets live in this file-scope array, one copy per GPU, for the whole process.
+// Host code never passes `scratch` itself to a kernel: fx_create resolves its device address on the
+// context's device (hipGetSymbolAddress) and every launch uses that address.
+#define FX_NOALLOC_PROW 516
+#define FX_NOALLOC_PARTIAL_BYTES ((size_t)FX_NOALLOC_MAX_SPLITS * 16 * FX_NOALLOC_PROW * 4)
+#define FX_NOALLOC_DONE_BYTES ((size_t)FX_WORKERS * 8)
+static __device__ __align__(256) uint8_t scratch[FX_NOALLOC_PARTIAL_BYTES + FX_NOALLOC_DONE_BYTES];
+
+// ------------------------------------------------------------------------------------------------
 // C ABI
 
 struct fx_ctx {
@@ -264,6 +274,7 @@ struct fx_ctx {
   int prof_iter = -1;
   rocblas_handle blas = nullptr;   // the prefill's GEMMs (created on first use)
   bool fp8 = false;                // the loaded plan's expert stages read FP8 weights
+  uint8_t* scratch = nullptr;      // device address of this device's `scratch` array
 };
 
 static int fail(fx_ctx* c, int code, const std::string& msg) {
@@ -311,6 +322,8 @@ int fx_create(int device, fx_ctx** out) {
   HIPCHK(c, hipMalloc(&c->timing, sizeof(uint64_t) * c->timing_cap));
   HIPCHK(c, hipEventCreate(&c->ev0));
   HIPCHK(c, hipEventCreate(&c->ev1));
+  // the allocation-free entry's scratch on this device (the context's device is current here)
+  HIPCHK(c, hipGetSymbolAddress((void**)&c->scratch, HIP_SYMBOL(scratch)));
   // the work split assumes block b runs on XCD b % 8 (round-robin dispatch); verify it once
   uint32_t* d = nullptr;
   HIPCHK(c, hipMalloc(&d, FX_BLOCKS * 4));
@@ -639,6 +652,59 @@ int fx_run_stage(fx_ctx* c, const fx_stage* st, int32_t step, uint32_t tbase, in
   uint32_t err = 0;
   HIPCHK(c, hipMemcpy(&err, c->err_flag, 4, hipMemcpyDeviceToHost));
   if (err) return fail(c, FX_E_STATE, "a packet wait timed out in the stage launch; create a new context");
+  return FX_OK;
+}
+
+// The attention pair of the kernel suite (an MLA_ATTEND stage, then its MLA_MERGE_UV stage) with
+// the split partials and the done packets in this device's `scratch` instead of caller buffers:
+// no allocation on any path. The attend stage runs with (tbase, sidx), the merge with
+// (tbase, sidx + 1) reading the attend stage's outputs; the stages' partials / done pointers are
+// ignored. At most FX_NOALLOC_MAX_SPLITS splits. Calls that overlap on one GPU race on `scratch`.
+int fx_mla_attend_merge_noalloc(fx_ctx* c, const fx_stage* attend, const fx_stage* merge, int32_t step,
+                                uint32_t tbase, int32_t sidx, void* stream) {
+  if (!c || !attend || !merge) return FX_E_ARG;
+  if (!c->scratch) return fail(c, FX_E_STATE, "the context has no scratch address");
+  if (attend->op != FX_OP_MLA_ATTEND || merge->op != FX_OP_MLA_MERGE_UV)
+    return fail(c, FX_E_ARG, "fx_mla_attend_merge_noalloc takes an MLA_ATTEND stage and an MLA_MERGE_UV stage");
+  if ((attend->flags & FX_F_MFMA) != (merge->flags & FX_F_MFMA))
+    return fail(c, FX_E_ARG, "the attend and merge stages must use the same attention kernel (FX_F_MFMA)");
+  if (attend->n_splits <= 0 || attend->n_splits > FX_NOALLOC_MAX_SPLITS || merge->n_splits != attend->n_splits ||
+      merge->split != attend->split)
+    return fail(c, FX_E_ARG, "n_splits must be in [1, " + std::to_string(FX_NOALLOC_MAX_SPLITS) +
+                                 "] and equal on both stages (the scratch holds that many splits' partials)");
+  if (attend->prow != FX_NOALLOC_PROW || merge->prow != FX_NOALLOC_PROW)
+    return fail(c, FX_E_ARG, "partials rows must be 516 floats (d_c = 512)");
+  if (step < 0 || (long long)step >= (long long)attend->n_splits * attend->split)
+    return fail(c, FX_E_ARG, "step outside the splits");
+  fx_stage a = *attend, m = *merge;
+  const uint64_t part = (uint64_t)c->scratch, done = part + FX_NOALLOC_PARTIAL_BYTES;
+  a.out = part;
+  a.aux[6] = done;
+  m.x = part;
+  m.aux[6] = done;
+  m.src[0] = sidx;
+  int r = check_stage(c, a, 0, 1 << 20);
+  if (r) return r;
+  r = check_stage(c, m, 1, 1 << 20);
+  if (r) return r;
+  hipStream_t s = (hipStream_t)stream;
+  // stale done packets of an earlier call could carry the tags this call waits for: zero them with a
+  // fill kernel (no memset node, so the call can be captured)
+  hipLaunchKernelGGL(fx_fill_kernel, dim3(1), dim3(256), 0, s, (uint16_t*)done, (uint64_t)(FX_NOALLOC_DONE_BYTES / 2),
+                     (uint16_t)0);
+  HIPCHK(c, hipGetLastError());
+  int32_t n_prompt = 1 << 30, sidx_m = sidx + 1;
+  int64_t* no_tokens = nullptr;
+  void* args_a[] = {(void*)&a, &step, &n_prompt, &tbase, &sidx, &no_tokens, &c->err_flag};
+  HIPCHK(c, hipLaunchCooperativeKernel((const void*)fx_stage_kernel, dim3(FX_BLOCKS), dim3(FX_THREADS), args_a,
+                                       FX_LDS_BYTES, s));
+  void* args_m[] = {(void*)&m, &step, &n_prompt, &tbase, &sidx_m, &no_tokens, &c->err_flag};
+  HIPCHK(c, hipLaunchCooperativeKernel((const void*)fx_stage_kernel, dim3(FX_BLOCKS), dim3(FX_THREADS), args_m,
+                                       FX_LDS_BYTES, s));
+  HIPCHK(c, hipStreamSynchronize(s));
+  uint32_t err = 0;
+  HIPCHK(c, hipMemcpy(&err, c->err_flag, 4, hipMemcpyDeviceToHost));
+  if (err) return fail(c, FX_E_STATE, "a packet wait timed out in the attention launch; create a new context");
   return FX_OK;
 }
 

@@ -102,6 +102,8 @@ def lib():
         "fx_set_profile": (ctypes.c_int, [vp, i32]),
         "fx_read_profile": (ctypes.c_int, [vp, ctypes.POINTER(ctypes.c_uint64), i32]),
         "fx_run_stage": (ctypes.c_int, [vp, ctypes.POINTER(FxStage), i32, ctypes.c_uint32, i32, vp]),
+        "fx_mla_attend_merge_noalloc": (ctypes.c_int, [vp, ctypes.POINTER(FxStage), ctypes.POINTER(FxStage), i32,
+                                                       ctypes.c_uint32, i32, vp]),
         "fx_time_stages": (ctypes.c_int, [vp, ctypes.POINTER(FxStage), i32, i32, i32, ctypes.c_uint32, i32, vp,
                                           ctypes.POINTER(ctypes.c_float)]),
         "fx_gen_normal_bf16": (ctypes.c_int, [vp, vp, u64, u64, u64, u64, u64, u64, ctypes.c_uint32, ctypes.c_float]),
@@ -133,7 +135,7 @@ def lib():
 EXPORTS = ("fx_abi_version", "fx_create", "fx_destroy", "fx_last_error", "fx_device_info", "fx_malloc", "fx_free",
            "fx_memcpy_htod", "fx_memcpy_dtoh", "fx_memcpy_dtod", "fx_memset", "fx_synchronize", "fx_load_plan",
            "fx_run", "fx_launch", "fx_finish", "fx_mark", "fx_marks_ms", "fx_last_run_ms", "fx_set_profile",
-           "fx_read_profile", "fx_read_timing", "fx_run_stage", "fx_time_stages", "fx_gen_normal_bf16", "fx_fill_u16",
+           "fx_read_profile", "fx_read_timing", "fx_run_stage", "fx_mla_attend_merge_noalloc", "fx_time_stages", "fx_gen_normal_bf16", "fx_fill_u16",
            "fx_quantize_fp8", "fx_dequantize_fp8", "fx_gemm", "fx_pf_embed", "fx_pf_rmsnorm", "fx_pf_prep", "fx_pf_softmax", "fx_pf_attn_out", "fx_pf_silu",
            "fx_pf_route", "fx_pf_gather", "fx_pf_combine")
 
@@ -243,6 +245,12 @@ class Runtime:
         """One stage as a standalone launch: packet inputs must carry tbase + src[k] + 1, outputs get
         tbase + sidx + 1."""
         self.check(self.L.fx_run_stage(self.h, ctypes.byref(stage), step, tbase, sidx, None), "fx_run_stage")
+
+    def attend_merge_noalloc(self, attend, merge, step=0, tbase=1000, sidx=5):
+        """The attend + merge stage pair with the library's own scratch for the split partials and
+        done packets (fx_mla_attend_merge_noalloc): no device allocation."""
+        self.check(self.L.fx_mla_attend_merge_noalloc(self.h, ctypes.byref(attend), ctypes.byref(merge), step, tbase,
+                                                      sidx, None), "fx_mla_attend_merge_noalloc")
 
     def time_stages(self, stages, reps=10, step=0, tbase=1000, sidx=5):
         """Mean µs per standalone launch of `stages` launched in turn, `reps` rounds (fx_time_stages)."""

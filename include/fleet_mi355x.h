@@ -215,6 +215,20 @@ int fx_read_timing(fx_ctx* ctx, uint64_t* buf, int32_t n);
  * is tokens(aux4)[step]. */
 int fx_run_stage(fx_ctx* ctx, const fx_stage* stage, int32_t step, uint32_t tbase, int32_t sidx, void* stream);
 
+/* Allocation-free attention (no counterpart in the reference; for callers that cannot allocate
+ * device memory: code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * The same work as fx_run_stage(attend) then fx_run_stage(merge) -- an MLA_ATTEND stage and its
+ * MLA_MERGE_UV stage, both with or both without FX_F_MFMA -- but the split partials and the done
+ * packets live in a library-owned device array (one per GPU, held until the process ends) instead
+ * of the stages' partials / done buffers, which are ignored; it calls no allocating routine. The
+ * attend stage runs with (tbase, sidx), the merge with (tbase, sidx + 1) and src[0] = sidx. Limit:
+ * n_splits <= FX_NOALLOC_MAX_SPLITS (the array holds that many splits' partials: 5.3 MB), partials
+ * rows of 516 floats; larger plans fail with FX_E_ARG. Every call on a GPU shares that GPU's array:
+ * calls that overlap on one GPU race. Returns after both launches have finished. */
+#define FX_NOALLOC_MAX_SPLITS 160
+int fx_mla_attend_merge_noalloc(fx_ctx* ctx, const fx_stage* attend, const fx_stage* merge, int32_t step,
+                                uint32_t tbase, int32_t sidx, void* stream);
+
 /* Kernel-suite timing (the reference suite's KT_TIME, fleet/tasks/README.md:294-311): `reps` rounds
  * of standalone launches of stages[0 .. n) in turn (n copies over different weights defeat the
  * 256 MB last-level cache), back to back on `stream`; *us = mean microseconds per launch from HIP
