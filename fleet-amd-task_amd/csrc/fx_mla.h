@@ -563,12 +563,19 @@ __device__ __forceinline__ void op_mla_attend(const fx_stage& s, FxEnv& env) {
 // sequential) -> bf16), then attn[h*d_v + v] = bf16(dot(o, W_uv[h][v])) for 8 rows v each
 // (harness/numpy_ref.py:168-174).
 #define MERGE_BATCH 40   // splits whose partials are requested at once (every live split up to ctx 1280)
+// With FX_F_MFMA the merge runs on workers 128..255 only, 8 per head (16 W_uv rows each): every
+// merge worker reads all of its head's partials, so fewer workers per head read fewer bytes, and the
+// attention's workers (0 .. live - 1) are not on the merge's critical path while live <= 128.
+#define MERGE_MFMA_FIRST 128
+#define MERGE_MFMA_PER_HEAD 8
 __device__ __forceinline__ void op_mla_merge_uv(const fx_stage& s, FxEnv& env) {
   const int nh = s.n_rows, d_c = s.d_c, d_v = s.d_n, prow = s.prow;
-  const int hh = env.xrank >> 4;
-  const int h = env.xcd * MLA_HP + hh;
-  const int v0 = (env.xrank & 15) * (d_v / 16);
-  const int nrows = d_v / 16;   // 8
+  const bool mfma = (s.flags & FX_F_MFMA) != 0;
+  if (mfma && env.worker < MERGE_MFMA_FIRST) return;
+  const int mw = env.worker - MERGE_MFMA_FIRST;
+  const int h = mfma ? mw / MERGE_MFMA_PER_HEAD : env.xcd * MLA_HP + (env.xrank >> 4);
+  const int nrows = mfma ? d_v / MERGE_MFMA_PER_HEAD : d_v / 16;   // 16 or 8
+  const int v0 = mfma ? (mw % MERGE_MFMA_PER_HEAD) * nrows : (env.xrank & 15) * nrows;
   const int live = (env.step + 1 + s.split - 1) / s.split;
   float* xs = (float*)(env.lds + LDS_XS);
   float* wj = (float*)(env.lds + LDS_TILE);
@@ -578,7 +585,7 @@ __device__ __forceinline__ void op_mla_merge_uv(const fx_stage& s, FxEnv& env) {
   const int ngroups = (nrows + 3) / 4;
   Tile<4, 1> t0;
   gemv_prime(t0, W, d_c, ngroups, rowof);
-  if (s.flags & FX_F_MFMA) {
+  if (mfma) {
     // split j ran on worker j % 256: the done packets of workers 0 .. min(live, 256) - 1
     if (wave_id() == 0)
       pk_wait_singles<4>((const void*)s.aux[6], lane_id(), 64, live < FX_WORKERS ? live : FX_WORKERS,
@@ -650,7 +657,7 @@ __device__ __forceinline__ void op_mla_merge_uv(const fx_stage& s, FxEnv& env) {
   const float den = red[0];
   xs[pc] = bf16r(num[0] / den);
   xs[pc + 1] = bf16r(num[1] / den);
-  if ((env.xrank & 15) == 0 && s.aux[4]) stc4((void*)s.aux[4], (uint32_t)(h * d_c + pc) * 2, pack2(xs[pc], xs[pc + 1]));
+  if (v0 == 0 && s.aux[4]) stc4((void*)s.aux[4], (uint32_t)(h * d_c + pc) * 2, pack2(xs[pc], xs[pc + 1]));
   __syncthreads();
   prof_mark(env, 5);
   float* o8 = red + 16;

@@ -116,7 +116,8 @@ enum fx_op {
 #define FX_F_MFMA 512u     /* MLA_ATTEND / MLA_MERGE_UV: the matrix-core attention. Split j runs on worker
                             * j % 256 for all heads (tiles of 32 positions; scores and value products on
                             * v_mfma_f32_16x16x32_bf16); done(aux6) holds one packet per worker, the merge
-                            * waits for workers 0 .. min(live splits, 256) - 1 */
+                            * waits for workers 0 .. min(live splits, 256) - 1 and runs on workers 128..255,
+                            * 8 per head (16 W_uv rows each) */
 
 /* One entry of the task table: one operator of the plan (fleet/graph_plan.py Call). */
 typedef struct fx_stage {
