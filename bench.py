@@ -159,8 +159,10 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--n-splits", type=int, default=None, help="attention split count (default: the plan's own)")
     ap.add_argument("--split", type=int, default=None, help="attention split length in positions (a multiple of 32)")
-    ap.add_argument("--attn", choices=("mfma", "valu"), default="mfma",
-                    help="attention kernel: matrix cores over all workers (mfma) or vector-ALU chains per XCD (valu)")
+    ap.add_argument("--attn", choices=("mfma", "xcd", "valu"), default=None,
+                    help="attention kernel: matrix cores over all workers (mfma), matrix cores with the merge on one "
+                         "XCD (xcd), or vector-ALU chains per XCD (valu); default: the plan's own choice for the "
+                         "cache length")
     ap.add_argument("--fp8-experts", action="store_true",
                     help="the experts' weights as FP8 (weight-only e4m3, per-row scales) instead of bf16")
     ap.add_argument("--fp8-head", action="store_true", help="the LM head's weights as FP8 too (implies --fp8-experts)")

@@ -57,24 +57,27 @@ __device__ __forceinline__ void am_issue_rows(u32x4* v, const uint16_t* ckv, con
     v[k] = c < 64 ? __builtin_amdgcn_raw_buffer_load_b128(rc, (uint32_t)(rr * 1024 + c * 16), 0, 0)
                   : __builtin_amdgcn_raw_buffer_load_b128(rk, (uint32_t)(rr * 128 + (c - 64) * 16), 0, 0);
   }
+  fx_issue_here();
 }
 
-// FX_OP_MLA_ATTEND with FX_F_MFMA: splits over all workers, every head per split. Partials as the
-// VALU form ([split][head][prow]: o, then lse); then one done packet per worker that owned a live
-// split, at done[worker] (the merge polls workers 0 .. min(live, 256) - 1).
-__device__ __forceinline__ void op_mla_attend_mfma(const fx_stage& s, FxEnv& env) {
+// The matrix-core attention of splits j = j0, j0 + jstep, .. below the live count, every head per
+// split. Inputs: q of every head (ql_nope packets, 2048 pairs, and q_pe packets aux[2], 256 pairs),
+// row `step` from the crow packets of this XCD (aux[5]); the cached rows from c_kv (aux[0]) and
+// k_pe (aux[1]). Partials ([split][head][prow]: o, then lse) are stored device-coherent, or
+// XCD-local (`local`: every reader runs on this XCD). after_q() runs once q is in LDS. Returns the
+// number of splits done; the caller waits for the stores and publishes its done packet.
+template <class AfterQ>
+__device__ __forceinline__ int am_attend(const fx_stage& s, FxEnv& env, const void* qln, void* part, int j0, int jstep,
+                                         bool local, uint32_t tin, AfterQ after_q) {
   const int step = env.step, split = s.split, prow = s.prow;
   const int n_live = (step + 1 + split - 1) / split;
-  if (env.worker >= n_live) return;
   const float scale = s.scale;
-  const uint32_t tin = tag_in(s, env, 0);
   char* lds = env.lds;
   const int lane = lane_id(), wave = wave_id();
   const int li = lane & 15, lg = lane >> 4;
   const uint16_t* ckv = (const uint16_t*)s.aux[0];
   const uint16_t* kpe = (const uint16_t*)s.aux[1];
   const void* crow = (const uint8_t*)s.aux[5] + (size_t)env.xcd * AM_DK / 2 * 8;
-  void* part = (void*)s.out;
   float* S = (float*)(lds + AM_S_OFF);
   float* H = (float*)(lds + AM_H_OFF);
   auto split_hi = [&](int j) { const int h = j * split + split; return h > step + 1 ? step + 1 : h; };
@@ -82,13 +85,13 @@ __device__ __forceinline__ void op_mla_attend_mfma(const fx_stage& s, FxEnv& env
   // the first tile's rows are requested before q is awaited
   u32x4 v[AM_LOADS];
   {
-    const int lo = env.worker * split;
-    am_issue_rows(v, ckv, kpe, lo, tile_n(lo, split_hi(env.worker)), step);
+    const int lo = j0 * split;
+    am_issue_rows(v, ckv, kpe, lo, tile_n(lo, split_hi(j0)), step);
   }
   // ---- q of every head: ql_nope (2048 pairs of packets) and q_pe (256 pairs), bf16 into LDS rows
   {
     u32x4 w[8];
-    pk_wait_pairs<8>((const void*)s.x, fx_tid(), FX_THREADS, 2048, tin, env.err, w);
+    pk_wait_pairs<8>(qln, fx_tid(), FX_THREADS, 2048, tin, env.err, w);
 #pragma unroll
     for (int n = 0; n < 8; ++n) {
       const int p = fx_tid() + n * FX_THREADS;      // pair p: head p / 128, columns 4 (p % 128) ..
@@ -105,8 +108,9 @@ __device__ __forceinline__ void op_mla_attend_mfma(const fx_stage& s, FxEnv& env
     *(u32x2*)(lds + AM_Q_OFF + (fx_tid() >> 4) * AM_ROW + 1024 + (fx_tid() & 15) * 8) = b;
   }
   prof_mark(env, 1);
+  after_q();
   int done = 0;
-  for (int j = env.worker; j < n_live; j += FX_WORKERS) {
+  for (int j = j0; j < n_live; j += jstep) {
     const int lo = j * split, hi = split_hi(j);
     // online-softmax state of head lg + 4 * wave (the same on the 16 lanes li of lane group lg)
     float m_run = -__builtin_inff(), l_run = 0.0f;
@@ -138,7 +142,7 @@ __device__ __forceinline__ void op_mla_attend_mfma(const fx_stage& s, FxEnv& env
         // request the next tile (this split's, or the worker's next split's first)
         int nt0 = t0 + AM_T, nhi = hi;
         if (nt0 >= hi) {
-          const int nj = j + FX_WORKERS;
+          const int nj = j + jstep;
           nt0 = nj * split;
           nhi = nj < n_live ? split_hi(nj) : 0;
         }
@@ -158,7 +162,6 @@ __device__ __forceinline__ void op_mla_attend_mfma(const fx_stage& s, FxEnv& env
         for (int jj = 0; jj < 4; ++jj) S[(4 * lg + jj) * AM_T + 16 * wave + li] = sc[jj] * scale;
       }
       __syncthreads();
-      if (done == 0 && t0 == lo) prof_mark(env, 4);
       // ---- softmax: lane (li, lg) of wave w takes head lg + 4 w, positions li and li + 16
       {
         const int h = lg + 4 * wave;
@@ -183,7 +186,6 @@ __device__ __forceinline__ void op_mla_attend_mfma(const fx_stage& s, FxEnv& env
         if (li == 0) H[h] = alpha;
       }
       __syncthreads();
-      if (done == 0 && t0 == lo) prof_mark(env, 5);
       // ---- value products: wave w, column tiles 128 w + 16 n; B rows read transposed
       {
         const fx_bf16x8 pf = lds_b128(lds + AM_P_OFF + li * AM_P_ROW + 16 * lg);
@@ -207,7 +209,6 @@ __device__ __forceinline__ void op_mla_attend_mfma(const fx_stage& s, FxEnv& env
           }
         }
       }
-      if (done == 0 && t0 == lo) prof_mark(env, 6);
     }
     // ---- o = acc / l, lse = m + log(l)
     __syncthreads();
@@ -224,17 +225,96 @@ __device__ __forceinline__ void op_mla_attend_mfma(const fx_stage& s, FxEnv& env
       for (int n = 0; n < 8; ++n) {
         const int c = 128 * wave + 16 * n + li;
 #pragma unroll
-        for (int jj = 0; jj < 4; ++jj) stcf(part, (uint32_t)((j * AM_NH + 4 * lg + jj) * prow + c), acc[n][jj] / linv[jj]);
+        for (int jj = 0; jj < 4; ++jj) {
+          const uint32_t off = (uint32_t)((j * AM_NH + 4 * lg + jj) * prow + c) * 4;
+          const uint32_t val = __float_as_uint(acc[n][jj] / linv[jj]);
+          if (local) stl4(part, off, val);
+          else stc4(part, off, val);
+        }
       }
-      if (fx_tid() < AM_NH)
-        stcf(part, (uint32_t)((j * AM_NH + fx_tid()) * prow + 512), H[16 + fx_tid()] + log_s(H[32 + fx_tid()]));
+      if (fx_tid() < AM_NH) {
+        const uint32_t off = (uint32_t)((j * AM_NH + fx_tid()) * prow + 512) * 4;
+        const uint32_t val = __float_as_uint(H[16 + fx_tid()] + log_s(H[32 + fx_tid()]));
+        if (local) stl4(part, off, val);
+        else stc4(part, off, val);
+      }
     }
     ++done;
   }
+  return done;
+}
+
+// FX_OP_MLA_ATTEND with FX_F_MFMA: splits over all workers (split j on worker j % 256), every head
+// per split. Partials as the VALU form ([split][head][prow]: o, then lse); then one done packet per
+// worker that owned a live split, at done[worker] (the merge polls workers 0 .. min(live, 256) - 1).
+__device__ __forceinline__ void op_mla_attend_mfma(const fx_stage& s, FxEnv& env) {
+  const int n_live = (env.step + 1 + s.split - 1) / s.split;
+  if (env.worker >= n_live) return;
+  const int done = am_attend(s, env, (const void*)s.x, (void*)s.out, env.worker, FX_WORKERS, false, tag_in(s, env, 0),
+                             [] {});
   // done packet of this worker: its partials are complete
   wait_mem();
   __syncthreads();
   prof_mark(env, 7);
   if (fx_tid() == 0) pk_put((void*)s.aux[6], (uint32_t)env.worker, (uint32_t)done, tag_out(env));
+  prof_mark(env, 2);
+}
+
+// FX_OP_MLA_MERGE_UV with FX_F_XCD: the attention of every head and its merge, both on the 32
+// workers of XCD FX_ATT_XCD, so that the partials and the done packets never leave that XCD's L2
+// (XCD-local stores, ~0.3 us from store to the reader's load against ~1.4 us device-coherent under
+// the weight stream). Split j runs on rank j % 32; rank r then merges head r / 2 and computes its
+// W_uv rows 64 (r % 2) .. + 63, whose weights are requested as soon as q has arrived. The stage
+// carries the attention's operands in the merge's spare fields: aux[3] = ql_nope packets (the
+// attention's x), aux[0] c_kv, aux[1] k_pe, aux[2] q_pe packets, aux[5] crow packets, scale; src[0]
+// = their producer (the prep). x = partials, aux[6] = done packets (one per rank), w = W_uv,
+// out = attn packets, aux[4] = o_merged dump or null.
+#define FX_ATT_XCD 7
+#define XCD_MERGE_ROWS 64
+__device__ __forceinline__ void op_mla_attend_merge_xcd(const fx_stage& s, FxEnv& env) {
+  if (env.xcd != FX_ATT_XCD) return;
+  const int d_c = s.d_c, d_v = s.d_n, nh = s.n_rows;
+  const int r = env.xrank;
+  const int live = (env.step + 1 + s.split - 1) / s.split;
+  const uint32_t tin = tag_in(s, env, 0), tout = tag_out(env);
+  const int h = r >> 1, v0 = (r & 1) * XCD_MERGE_ROWS;
+  const uint16_t* W = (const uint16_t*)s.w + (size_t)h * d_v * d_c;
+  // wave w: W_uv rows v0 + 16 w .. + 15 (one 16-row group per wave, K = 512: one chunk per lane)
+  auto rowof = [&](int g, int i) { return v0 + 16 * g + i; };
+  Tile<16, 1> tw;
+  auto prime = [&] { tile_load(tw, W, d_c, wave_id(), rowof); };
+  void* part = (void*)s.x;
+  int done = 0;
+  if (r < live) done = am_attend(s, env, (const void*)s.aux[3], part, r, FX_XWORKERS, true, tin, prime);
+  else prime();
+  // this rank's partials are complete (the store counter drains in order, the W_uv rows with it:
+  // they were requested before the first tile was scored)
+  wait_mem();
+  __syncthreads();
+  prof_mark(env, 4);
+  if (fx_tid() == 0 && r < live) pk_put((void*)s.aux[6], (uint32_t)r, (uint32_t)done, tout, true);
+  if (wave_id() == 0)
+    pk_wait_singles<1>((const void*)s.aux[6], lane_id(), 64, live < FX_XWORKERS ? live : FX_XWORKERS, tout, env.err);
+  __syncthreads();
+  prof_mark(env, 5);
+  float* xs = (float*)(env.lds + LDS_XS);
+  merge_head(part, nh, h, s.prow, d_c, live, xs, (float*)(env.lds + LDS_TILE), (float*)(env.lds + LDS_RED));
+  if (v0 == 0 && s.aux[4])
+    stc4((void*)s.aux[4], (uint32_t)(h * d_c + fx_tid() * 2) * 2, pack2(xs[fx_tid() * 2], xs[fx_tid() * 2 + 1]));
+  __syncthreads();
+  prof_mark(env, 6);
+  float* o8 = (float*)(env.lds + LDS_RED) + 16;
+  {
+    float acc[16];
+    tile_dot(tw, xs, d_c, acc);
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      if (lane_id() == 0) o8[16 * wave_id() + i] = bf16r(acc[i]);
+  }
+  __syncthreads();
+  if (fx_tid() < XCD_MERGE_ROWS / 4) {
+    const float* o = o8 + 4 * fx_tid();
+    pk_put2((void*)s.out, (uint32_t)((h * d_v + v0) / 2 + 2 * fx_tid()), pack2(o[0], o[1]), pack2(o[2], o[3]), tout);
+  }
   prof_mark(env, 2);
 }

@@ -125,6 +125,20 @@ __device__ __forceinline__ void stc4(void* base, uint32_t off, uint32_t v) {
 __device__ __forceinline__ void stc2(void* base, uint32_t off, uint32_t v) {
   __builtin_amdgcn_raw_buffer_store_b16((unsigned short)v, rsrc(base), off, 0, FX_SC1);
 }
+// XCD-local stores (sc0): the data stays in this XCD's L2, where the sc1 loads of workgroups on the
+// same XCD find it (a flag round trip this way takes ~0.63 us, idle or under a full-chip weight
+// stream, against 1.0 / 2.8 us with sc1 stores); workgroups on other XCDs do not see it until the
+// line leaves the L2. Used only for data whose every reader runs on the writer's XCD.
+#define FX_SC0 1
+__device__ __forceinline__ void stl16(void* base, uint32_t off, u32x4 v) {
+  __builtin_amdgcn_raw_buffer_store_b128(v, rsrc(base), off, 0, FX_SC0);
+}
+__device__ __forceinline__ void stl8(void* base, uint32_t off, u32x2 v) {
+  __builtin_amdgcn_raw_buffer_store_b64(v, rsrc(base), off, 0, FX_SC0);
+}
+__device__ __forceinline__ void stl4(void* base, uint32_t off, uint32_t v) {
+  __builtin_amdgcn_raw_buffer_store_b32(v, rsrc(base), off, 0, FX_SC0);
+}
 __device__ __forceinline__ float ldcf(const void* base, uint32_t idx) { return __uint_as_float(ldc4(base, idx * 4)); }
 __device__ __forceinline__ void stcf(void* base, uint32_t idx, float v) { stc4(base, idx * 4, __float_as_uint(v)); }
 
@@ -141,20 +155,24 @@ __device__ __forceinline__ void wait_mem() { __builtin_amdgcn_s_waitcnt(0); }
 // packets: 8 bytes = 32-bit payload | 32-bit tag of the producing stage. Stored and loaded with
 // sc1, two packets per 16-byte access (the tag of each packet is checked on its own).
 
-__device__ __forceinline__ void pk_put(void* base, uint32_t pkt, uint32_t payload, uint32_t tag) {
+// local: every reader of the packet runs on this XCD (stored with sc0, see stl16)
+__device__ __forceinline__ void pk_put(void* base, uint32_t pkt, uint32_t payload, uint32_t tag, bool local = false) {
   u32x2 v;
   v.x = payload;
   v.y = tag;
-  stc8(base, pkt * 8u, v);
+  if (local) stl8(base, pkt * 8u, v);
+  else stc8(base, pkt * 8u, v);
 }
 // packets pkt, pkt + 1 (pkt even)
-__device__ __forceinline__ void pk_put2(void* base, uint32_t pkt, uint32_t p0, uint32_t p1, uint32_t tag) {
+__device__ __forceinline__ void pk_put2(void* base, uint32_t pkt, uint32_t p0, uint32_t p1, uint32_t tag,
+                                        bool local = false) {
   u32x4 v;
   v.x = p0;
   v.y = tag;
   v.z = p1;
   v.w = tag;
-  stc16(base, pkt * 8u, v);
+  if (local) stl16(base, pkt * 8u, v);
+  else stc16(base, pkt * 8u, v);
 }
 
 // Wait until packets pkt, pkt + 1 (pkt even) carry `tag`; returns them (payloads in .x, .z).
@@ -265,6 +283,12 @@ __device__ __forceinline__ uint32_t pk_wait1(const void* base, uint32_t pkt, uin
 // access would wait for the weight loads still in flight.
 typedef const __attribute__((address_space(1))) u32x4* gptr16;
 __device__ __forceinline__ u32x4 ldw16(const void* p) { return __builtin_nontemporal_load((gptr16)p); }
+// Keeps the loads issued before it where the source issues them. Without it the compiler may sink a
+// prefetch (the next weight tile, the next cache rows) past the packet polls and barriers that
+// follow, down to its first use: the load then starts only when its data is needed and its whole
+// latency is exposed. An empty asm with a memory clobber is a compiler-only fence: it emits no
+// instruction and no wait.
+__device__ __forceinline__ void fx_issue_here() { asm volatile("" ::: "memory"); }
 __device__ __forceinline__ u32x4 ld16(const void* p) { return *(gptr16)p; }
 
 // ------------------------------------------------------------------------------------------------
@@ -303,9 +327,8 @@ __device__ __forceinline__ float xor_lane(float v) {
   if constexpr (O == 1) return dpp_mov<0xB1>(v);          // quad_perm [1,0,3,2]
   else if constexpr (O == 2) return dpp_mov<0x4E>(v);     // quad_perm [2,3,0,1]
   else if constexpr (O == 4) {
-    const float up = dpp_mov<0x104>(v);                   // row_shl:4  (lane + 4)
-    const float dn = dpp_mov<0x114>(v);                   // row_shr:4  (lane - 4)
-    return (fx_tid() & 4) ? dn : up;
+    // row_half_mirror (lane i of 8 <- 7 - i = i ^ 7), then quad_perm [3,2,1,0] (i <- i ^ 3): i ^ 4
+    return dpp_mov<0x1B>(dpp_mov<0x141>(v));
   } else if constexpr (O == 8) return dpp_mov<0x128>(v);  // row_ror:8 (lane ^ 8 inside 16)
   else if constexpr (O == 16) {
     // odd rows of the first operand <-> even rows of the second: [0] = rows (0, 0, 2, 2), [1] = (1, 1, 3, 3)
@@ -320,31 +343,83 @@ __device__ __forceinline__ float xor_lane(float v) {
   }
 }
 
+// Both outputs of the row swap of v with itself (as floats in o0, o1): per lane, one holds the
+// lane's own value and the other its partner's (lane ^ 16, or lane ^ 32). Each output goes through
+// a scalar (__uint_as_float by value): __builtin_bit_cast of a vector element reads the vector's
+// first element whatever the index, so both outputs would come out as the first.
+template <int O>
+__device__ __forceinline__ void swap_pair(float v, float& o0, float& o1) {
+  const unsigned a = __float_as_uint(v);
+  if constexpr (O == 16) {
+    const auto t = __builtin_amdgcn_permlane16_swap(a, a, false, false);
+    const unsigned t0 = t[0], t1 = t[1];
+    o0 = __uint_as_float(t0);
+    o1 = __uint_as_float(t1);
+  } else {
+    const auto t = __builtin_amdgcn_permlane32_swap(a, a, false, false);
+    const unsigned t0 = t[0], t1 = t[1];
+    o0 = __uint_as_float(t0);
+    o1 = __uint_as_float(t1);
+  }
+}
+// v + xor_lane<O>(v) on every lane. For O = 16 / 32 the sum of the swap's two outputs is the lane's
+// own value plus its partner's on every lane: IEEE addition is commutative, so this is bit for bit
+// the same sum, without the per-lane select of xor_lane.
+template <int O>
+__device__ __forceinline__ float add_xor(float v) {
+  if constexpr (O == 16 || O == 32) {
+    float o0, o1;
+    swap_pair<O>(v, o0, o1);
+    return o0 + o1;
+  } else {
+    return v + xor_lane<O>(v);
+  }
+}
+// max(v, xor_lane<O>(v)) on every lane (the same select-free form; max is commutative)
+template <int O>
+__device__ __forceinline__ float max_xor(float v) {
+  if constexpr (O == 16 || O == 32) {
+    float o0, o1;
+    swap_pair<O>(v, o0, o1);
+    return fmaxf(o0, o1);
+  } else {
+    return fmaxf(v, xor_lane<O>(v));
+  }
+}
+
 // xor butterfly over the lowest `nl` lanes of each 64-lane group (spec order 1, 2, 4, ..): the
 // balanced pairwise tree over lanes; every lane ends with the same sum
 __device__ __forceinline__ float butterfly(float v, int nl) {
-  if (nl > 1) v = v + xor_lane<1>(v);
-  if (nl > 2) v = v + xor_lane<2>(v);
-  if (nl > 4) v = v + xor_lane<4>(v);
-  if (nl > 8) v = v + xor_lane<8>(v);
-  if (nl > 16) v = v + xor_lane<16>(v);
-  if (nl > 32) v = v + xor_lane<32>(v);
+  if (nl > 1) v = add_xor<1>(v);
+  if (nl > 2) v = add_xor<2>(v);
+  if (nl > 4) v = add_xor<4>(v);
+  if (nl > 8) v = add_xor<8>(v);
+  if (nl > 16) v = add_xor<16>(v);
+  if (nl > 32) v = add_xor<32>(v);
   return v;
 }
-__device__ __forceinline__ float butterfly64(float v) { return butterfly(v, 64); }
+// the same over all 64 lanes, with no test (nl is a runtime value in butterfly: each test would be
+// a branch per row and level)
+__device__ __forceinline__ float butterfly64(float v) {
+  v = add_xor<1>(v);
+  v = add_xor<2>(v);
+  v = add_xor<4>(v);
+  v = add_xor<8>(v);
+  v = add_xor<16>(v);
+  return add_xor<32>(v);
+}
 __device__ __forceinline__ int lanes_for(int nchunk) {
   int nl = 1;
   while (nl < nchunk && nl < 64) nl <<= 1;
   return nl;
 }
 __device__ __forceinline__ float wave_max(float v) {
-  v = fmaxf(v, xor_lane<1>(v));
-  v = fmaxf(v, xor_lane<2>(v));
-  v = fmaxf(v, xor_lane<4>(v));
-  v = fmaxf(v, xor_lane<8>(v));
-  v = fmaxf(v, xor_lane<16>(v));
-  v = fmaxf(v, xor_lane<32>(v));
-  return v;
+  v = max_xor<1>(v);
+  v = max_xor<2>(v);
+  v = max_xor<4>(v);
+  v = max_xor<8>(v);
+  v = max_xor<16>(v);
+  return max_xor<32>(v);
 }
 
 // 8 fma of a bf16 chunk (4 words) with 8 f32 values, chunk order e = 0..7

@@ -55,6 +55,7 @@ __device__ __forceinline__ void tile_load(Tile<R, NJ>& t, const uint16_t* __rest
       t.w[i][j] = ldw16(W + (size_t)r * K + (size_t)cc * 8);
     }
   }
+  fx_issue_here();
 }
 
 template <int R, int NJ>
@@ -74,9 +75,14 @@ __device__ __forceinline__ void tile_dot(const Tile<R, NJ>& t, const float* xs, 
       for (int i = 0; i < R; ++i) acc[i] = fma8(t.w[i][j], xv, acc[i]);
     }
   }
-  const int nl = lanes_for(nchunk);
+  if (nchunk >= 64) {
 #pragma unroll
-  for (int i = 0; i < R; ++i) acc[i] = butterfly(acc[i], nl);
+    for (int i = 0; i < R; ++i) acc[i] = butterfly64(acc[i]);
+  } else {
+    const int nl = lanes_for(nchunk);
+#pragma unroll
+    for (int i = 0; i < R; ++i) acc[i] = butterfly(acc[i], nl);
+  }
 }
 
 template <int R, int NJ, class RowFn>
@@ -101,6 +107,7 @@ __device__ __forceinline__ void tile_load(TileQ<R, NJ>& t, const Fp8W& W, int K,
   }
 #pragma unroll
   for (int i = 0; i < R; ++i) t.sc[i] = W.s[t.row[i] >= 0 ? t.row[i] : first];
+  fx_issue_here();
 }
 
 // the 16 codes of a chunk as f32 (the hardware's OCP e4m3fn conversion, byte k = element k)
@@ -139,9 +146,14 @@ __device__ __forceinline__ void tile_dot(const TileQ<R, NJ>& t, const float* xs,
       }
     }
   }
-  const int nl = lanes_for(nchunk);
+  if (nchunk >= 64) {
 #pragma unroll
-  for (int i = 0; i < R; ++i) acc[i] = butterfly(acc[i], nl) * t.sc[i];
+    for (int i = 0; i < R; ++i) acc[i] = butterfly64(acc[i]) * t.sc[i];
+  } else {
+    const int nl = lanes_for(nchunk);
+#pragma unroll
+    for (int i = 0; i < R; ++i) acc[i] = butterfly(acc[i], nl) * t.sc[i];
+  }
 }
 
 // Issue the loads of this wave's first group (group index = wave id) into t0.
@@ -287,6 +299,7 @@ __device__ __forceinline__ NormW norm_prefetch(const uint16_t* wn, int K) {
   NormW n;
   n.w = u32x4{0u, 0u, 0u, 0u};
   if (fx_tid() * 8 < K) n.w = ld16(wn + fx_tid() * 8);
+  fx_issue_here();
   return n;
 }
 __device__ __forceinline__ void rmsnorm_pre(float* xs, const NormW& n, int K, float eps, float* red) {
@@ -360,7 +373,13 @@ __device__ __forceinline__ void op_gemv_w(const fx_stage& s, FxEnv& env, const W
   float* rres = (float*)(env.lds + LDS_RES);
   const int K = s.k;
   int g0, g1;
-  range_split((s.n_rows + 3) >> 2, env.nworkers, env.worker, g0, g1);
+  if (s.flags & FX_F_SKIP_XCD) {
+    // the workers of XCDs 0..6 (rank r of XCD x is worker r * 7 + x of 224)
+    if (env.xcd == FX_XCDS - 1) return;
+    range_split((s.n_rows + 3) >> 2, env.nworkers - FX_XWORKERS, env.xrank * (FX_XCDS - 1) + env.xcd, g0, g1);
+  } else {
+    range_split((s.n_rows + 3) >> 2, env.nworkers, env.worker, g0, g1);
+  }
   const int r0 = g0 * 4, r1 = g1 * 4 < s.n_rows ? g1 * 4 : s.n_rows;
   const int ngroups = (r1 - r0 + R - 1) / R;
   auto rowof = [&](int g, int i) { const int r = r0 + g * R + i; return r < r1 ? r : -1; };

@@ -33,6 +33,8 @@ __device__ __forceinline__ void op_mla_prep(const fx_stage& s, FxEnv& env) {
   const int h0 = env.xcd * MLA_HP;
   const void* qkva = (const void*)s.x;
   const uint32_t tin = tag_in(s, env, 0), tout = tag_out(env);
+  // FX_F_XLOCAL: the packets are read by the same XCD's attention only (heads 2x, 2x + 1 on XCD x)
+  const bool loc = (__builtin_amdgcn_readfirstlane(s.flags) & FX_F_XLOCAL) != 0;
   if (env.xrank != PREP_ROW_RANK) {
     const int t = env.xrank + (PREP_ROW_RANK)*wave_id();
     if (t >= MLA_HP * (d_c / 32)) return;
@@ -44,6 +46,7 @@ __device__ __forceinline__ void op_mla_prep(const fx_stage& s, FxEnv& env) {
     u32x4 wr[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) wr[e] = ldw16(Wh + (size_t)(8 * k + e) * d_c + c0);
+    fx_issue_here();
     // q_nope[h][8k .. 8k + 8): pairs (h * qstride + 8k) / 4, + 1
     u32x4 qv[2];
     pk_wait_pairs<2>(qkva, (h * qstride + 8 * k) >> 2, 1, q_out >> 2, tin, env.err, qv);
@@ -64,8 +67,8 @@ __device__ __forceinline__ void op_mla_prep(const fx_stage& s, FxEnv& env) {
     for (int c = 0; c < 8; ++c) acc[c] = butterfly(acc[c], 16);
     if (k == 0) {
       const uint32_t pkt = (uint32_t)(h * d_c + c0) >> 1;
-      pk_put2((void*)s.out, pkt, pack2(acc[0], acc[1]), pack2(acc[2], acc[3]), tout);
-      pk_put2((void*)s.out, pkt + 2, pack2(acc[4], acc[5]), pack2(acc[6], acc[7]), tout);
+      pk_put2((void*)s.out, pkt, pack2(acc[0], acc[1]), pack2(acc[2], acc[3]), tout, loc);
+      pk_put2((void*)s.out, pkt + 2, pack2(acc[4], acc[5]), pack2(acc[6], acc[7]), tout, loc);
     }
     prof_mark(env, 2);
     return;
@@ -85,6 +88,7 @@ __device__ __forceinline__ void op_mla_prep(const fx_stage& s, FxEnv& env) {
     rc = bf2f(cosr[fx_tid() % d_r]);
     rsn = bf2f(sinr[fx_tid() % d_r]);
   }
+  fx_issue_here();
   {
     // pairs: latent (q_out .. q_out + d_c) -> 128, k_pe -> 16, q_pe of the two heads -> 2 x 16
     const int t = fx_tid();
@@ -131,12 +135,13 @@ __device__ __forceinline__ void op_mla_prep(const fx_stage& s, FxEnv& env) {
   void* crow = (uint8_t*)s.aux[5] + (size_t)env.xcd * (d_c + d_r) / 2 * 8;
   for (int t = fx_tid(); t < (d_c + d_r) / 4; t += FX_THREADS) {
     const float* r = t < d_c / 4 ? xs + 4 * t : rp + 4 * (t - d_c / 4);
-    pk_put2(crow, (uint32_t)(2 * t), pack2(r[0], r[1]), pack2(r[2], r[3]), tout);
+    pk_put2(crow, (uint32_t)(2 * t), pack2(r[0], r[1]), pack2(r[2], r[3]), tout, loc);
   }
   if (fx_tid() < MLA_HP * d_r / 4) {
     const int hh = fx_tid() / (d_r / 4), j = fx_tid() % (d_r / 4);
     const float* r = rp + 64 + hh * 64 + 4 * j;
-    pk_put2((void*)s.aux[2], (uint32_t)(((h0 + hh) * d_r) / 2 + 2 * j), pack2(r[0], r[1]), pack2(r[2], r[3]), tout);
+    pk_put2((void*)s.aux[2], (uint32_t)(((h0 + hh) * d_r) / 2 + 2 * j), pack2(r[0], r[1]), pack2(r[2], r[3]), tout,
+            loc);
   }
   prof_mark(env, 2);
 }
@@ -172,6 +177,7 @@ __device__ __forceinline__ void att_issue_rows(u32x4* v, const uint16_t* ckv, co
     if (rr < 0) { v[k] = (u32x4){0u, 0u, 0u, 0u}; continue; }   // no cached row yet (step == t0)
     v[k] = c < 64 ? ld16(ckv + (size_t)rr * d_c + c * 8) : ld16(kpe + (size_t)rr * d_r + (c - 64) * 8);
   }
+  fx_issue_here();
 }
 
 // FX_OP_MLA_ATTEND. A worker walks its splits j = xrank, xrank + 32, .. in passes of up to two
@@ -544,8 +550,9 @@ __device__ __forceinline__ void op_mla_attend(const fx_stage& s, FxEnv& env) {
       o.y = __float_as_uint(acc[1] / l);
       o.z = __float_as_uint(acc[2] / l);
       o.w = __float_as_uint(acc[3] / l);
-      stc16(part, (base + pc) * 4, o);
-      if ((fx_tid() & 127) == 0) stcf(part, base + d_c, hs[ph * 4 + 0] + log_s(l));
+      // read only by this XCD's merge (its heads): XCD-local stores
+      stl16(part, (base + pc) * 4, o);
+      if ((fx_tid() & 127) == 0) stl4(part, (base + d_c) * 4, __float_as_uint(hs[ph * 4 + 0] + log_s(l)));
     }
     ++done;
   }
@@ -554,52 +561,17 @@ __device__ __forceinline__ void op_mla_attend(const fx_stage& s, FxEnv& env) {
   __syncthreads();
   prof_mark(env, 7);
   if (fx_tid() == 0)
-    pk_put((void*)s.aux[6], (uint32_t)(env.xcd * FX_XWORKERS + env.xrank), (uint32_t)done, tag_out(env));
+    pk_put((void*)s.aux[6], (uint32_t)(env.xcd * FX_XWORKERS + env.xrank), (uint32_t)done, tag_out(env), true);
   prof_mark(env, 2);
 }
 
-// FX_OP_MLA_MERGE_UV: ranks 0..15 / 16..31 of XCD x merge head 2x / 2x + 1 (harness/numpy_ref.py:
-// 152-165: M = max lse, w_j = exp(lse_j - M), o = (sum_j w_j o_j, sequential fma) / (sum_j w_j,
-// sequential) -> bf16), then attn[h*d_v + v] = bf16(dot(o, W_uv[h][v])) for 8 rows v each
-// (harness/numpy_ref.py:168-174).
+// The merge of head h (harness/numpy_ref.py:152-165): M = max lse, w_j = exp(lse_j - M), o = (sum_j
+// w_j o_j, sequential fma) / (sum_j w_j, sequential) -> bf16, over the first `live` splits' partials
+// ([split][head][prow]: o, then lse). xs[0, d_c) receives o (thread t: columns 2t, 2t + 1); wj
+// (LDS, live floats) and red[0] are scratch. The caller syncs before reading xs.
 #define MERGE_BATCH 40   // splits whose partials are requested at once (every live split up to ctx 1280)
-// With FX_F_MFMA the merge runs on workers 128..255 only, 8 per head (16 W_uv rows each): every
-// merge worker reads all of its head's partials, so fewer workers per head read fewer bytes, and the
-// attention's workers (0 .. live - 1) are not on the merge's critical path while live <= 128.
-#define MERGE_MFMA_FIRST 128
-#define MERGE_MFMA_PER_HEAD 8
-__device__ __forceinline__ void op_mla_merge_uv(const fx_stage& s, FxEnv& env) {
-  const int nh = s.n_rows, d_c = s.d_c, d_v = s.d_n, prow = s.prow;
-  const bool mfma = (s.flags & FX_F_MFMA) != 0;
-  if (mfma && env.worker < MERGE_MFMA_FIRST) return;
-  const int mw = env.worker - MERGE_MFMA_FIRST;
-  const int h = mfma ? mw / MERGE_MFMA_PER_HEAD : env.xcd * MLA_HP + (env.xrank >> 4);
-  const int nrows = mfma ? d_v / MERGE_MFMA_PER_HEAD : d_v / 16;   // 16 or 8
-  const int v0 = mfma ? (mw % MERGE_MFMA_PER_HEAD) * nrows : (env.xrank & 15) * nrows;
-  const int live = (env.step + 1 + s.split - 1) / s.split;
-  float* xs = (float*)(env.lds + LDS_XS);
-  float* wj = (float*)(env.lds + LDS_TILE);
-  float* red = (float*)(env.lds + LDS_RED);
-  const uint16_t* W = (const uint16_t*)s.w + (size_t)h * d_v * d_c;
-  auto rowof = [&](int g, int i) { const int r = v0 + g * 4 + i; return r < v0 + nrows ? r : -1; };
-  const int ngroups = (nrows + 3) / 4;
-  Tile<4, 1> t0;
-  gemv_prime(t0, W, d_c, ngroups, rowof);
-  if (mfma) {
-    // split j ran on worker j % 256: the done packets of workers 0 .. min(live, 256) - 1
-    if (wave_id() == 0)
-      pk_wait_singles<4>((const void*)s.aux[6], lane_id(), 64, live < FX_WORKERS ? live : FX_WORKERS,
-                         tag_in(s, env, 0), env.err);
-  } else if (wave_id() == 0) {
-    // the XCD's 32 done packets
-    u32x4 v[1];
-    const int first = env.xcd * FX_XWORKERS / 2;
-    pk_wait_pairs<1>((const void*)s.aux[6], first + (lane_id() & 15), 0, first + FX_XWORKERS / 2, tag_in(s, env, 0),
-                     env.err, v);
-  }
-  __syncthreads();
-  prof_mark(env, 1);
-  const void* part = (const void*)s.x;
+__device__ __forceinline__ void merge_head(const void* part, int nh, int h, int prow, int d_c, int live, float* xs,
+                                           float* wj, float* red) {
   // wave 0 requests the lse of splits lane, lane + 64 first: loads complete in issue order, so the
   // weights below need not wait for the wave's partial-o loads
   float l0 = -__builtin_inff(), l1 = -__builtin_inff();
@@ -636,7 +608,6 @@ __device__ __forceinline__ void op_mla_merge_uv(const fx_stage& s, FxEnv& env) {
     if (lane_id() == 0) red[0] = den;
   }
   __syncthreads();
-  prof_mark(env, 4);
   // num = sum_j w_j o_j[c] in j order (fma)
   float num[2] = {0.0f, 0.0f};
   for (int j0 = 0; j0 < live; j0 += MERGE_BATCH) {
@@ -657,6 +628,47 @@ __device__ __forceinline__ void op_mla_merge_uv(const fx_stage& s, FxEnv& env) {
   const float den = red[0];
   xs[pc] = bf16r(num[0] / den);
   xs[pc + 1] = bf16r(num[1] / den);
+}
+
+// FX_OP_MLA_MERGE_UV: ranks 0..15 / 16..31 of XCD x merge head 2x / 2x + 1 (merge_head), then
+// attn[h*d_v + v] = bf16(dot(o, W_uv[h][v])) for 8 rows v each (harness/numpy_ref.py:168-174).
+// With FX_F_MFMA the merge runs on workers 128..255 only, 8 per head (16 W_uv rows each): every
+// merge worker reads all of its head's partials, so fewer workers per head read fewer bytes, and the
+// attention's workers (0 .. live - 1) are not on the merge's critical path while live <= 128.
+#define MERGE_MFMA_FIRST 128
+#define MERGE_MFMA_PER_HEAD 8
+__device__ __forceinline__ void op_mla_merge_uv(const fx_stage& s, FxEnv& env) {
+  const int nh = s.n_rows, d_c = s.d_c, d_v = s.d_n, prow = s.prow;
+  const bool mfma = (s.flags & FX_F_MFMA) != 0;
+  if (mfma && env.worker < MERGE_MFMA_FIRST) return;
+  const int mw = env.worker - MERGE_MFMA_FIRST;
+  const int h = mfma ? mw / MERGE_MFMA_PER_HEAD : env.xcd * MLA_HP + (env.xrank >> 4);
+  const int nrows = mfma ? d_v / MERGE_MFMA_PER_HEAD : d_v / 16;   // 16 or 8
+  const int v0 = mfma ? (mw % MERGE_MFMA_PER_HEAD) * nrows : (env.xrank & 15) * nrows;
+  const int live = (env.step + 1 + s.split - 1) / s.split;
+  float* xs = (float*)(env.lds + LDS_XS);
+  float* red = (float*)(env.lds + LDS_RED);
+  const uint16_t* W = (const uint16_t*)s.w + (size_t)h * d_v * d_c;
+  auto rowof = [&](int g, int i) { const int r = v0 + g * 4 + i; return r < v0 + nrows ? r : -1; };
+  const int ngroups = (nrows + 3) / 4;
+  Tile<4, 1> t0;
+  gemv_prime(t0, W, d_c, ngroups, rowof);
+  if (mfma) {
+    // split j ran on worker j % 256: the done packets of workers 0 .. min(live, 256) - 1
+    if (wave_id() == 0)
+      pk_wait_singles<4>((const void*)s.aux[6], lane_id(), 64, live < FX_WORKERS ? live : FX_WORKERS,
+                         tag_in(s, env, 0), env.err);
+  } else if (wave_id() == 0) {
+    // the XCD's 32 done packets
+    u32x4 v[1];
+    const int first = env.xcd * FX_XWORKERS / 2;
+    pk_wait_pairs<1>((const void*)s.aux[6], first + (lane_id() & 15), 0, first + FX_XWORKERS / 2, tag_in(s, env, 0),
+                     env.err, v);
+  }
+  __syncthreads();
+  prof_mark(env, 1);
+  merge_head((const void*)s.x, nh, h, prow, d_c, live, xs, (float*)(env.lds + LDS_TILE), red);
+  const int pc = fx_tid() * 2;
   if (v0 == 0 && s.aux[4]) stc4((void*)s.aux[4], (uint32_t)(h * d_c + pc) * 2, pack2(xs[pc], xs[pc + 1]));
   __syncthreads();
   prof_mark(env, 5);

@@ -4,7 +4,7 @@
 //   fx_gemv.h  GEMV (qkva, o_proj, dense down, LM head + argmax), dense gate|up + SiLU
 //   fx_moe.h   router, expert gate|up + SiLU, expert down + combine, argmax reduce
 //   fx_mla.h   MLA prep (norm, RoPE, cache append, W_uk absorb), split-KV attend, LSE merge + W_uv
-//   fx_attn.h  split-KV attend on the matrix cores (FX_F_MFMA)
+//   fx_attn.h  split-KV attend on the matrix cores (FX_F_MFMA), and with its merge on one XCD (FX_F_XCD)
 #pragma once
 #include "fx_attn.h"
 #include "fx_moe.h"
@@ -22,10 +22,15 @@ __device__ __forceinline__ void run_stage(const fx_stage& s, FxEnv& env) {
       break;
     case FX_OP_MLA_PREP: op_mla_prep(s, env); break;
     case FX_OP_MLA_ATTEND:
+      // FX_F_XCD: the attention runs inside the merge stage that follows
+      if (s.flags & FX_F_XCD) break;
       if (s.flags & FX_F_MFMA) op_mla_attend_mfma(s, env);
       else op_mla_attend(s, env);
       break;
-    case FX_OP_MLA_MERGE_UV: op_mla_merge_uv(s, env); break;
+    case FX_OP_MLA_MERGE_UV:
+      if (s.flags & FX_F_XCD) op_mla_attend_merge_xcd(s, env);
+      else op_mla_merge_uv(s, env);
+      break;
     case FX_OP_MOE_ROUTER: op_moe_router(s, env); break;
     case FX_OP_MOE_W13: op_moe_w13<kFp8>(s, env); break;
     case FX_OP_MOE_W2: op_moe_w2<kFp8>(s, env); break;

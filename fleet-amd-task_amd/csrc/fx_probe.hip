@@ -200,8 +200,30 @@ __global__ void fxp_chase_kernel(const uint32_t* idx, uint32_t hops, int mode, c
 // ---- ping-pong between block a and block b (cooperative launch of `grid` blocks): a stores
 // flag[0] = i, b waits for it and stores flag[32] = i, a waits; `rounds` round trips, stamped by a.
 // Other blocks stream-read `load` while the exchange runs (if non-null).
-__global__ void fxp_pingpong_kernel(uint32_t* flag, int a, int b, uint32_t rounds, const uint8_t* load, uint64_t load_bytes,
-                                    uint64_t* out) {
+// mode 0: agent-scope relaxed atomics; 1: buffer loads with sc0 and plain buffer stores; 2: buffer
+// loads and stores with sc1 (the packet policy of the decode kernel); 3: plain buffer stores, and
+// loads after an invalidate of the CU's L1 (buffer_inv sc0); 4: buffer loads and stores with sc0;
+// 5: stores with sc1, loads with sc0; 6: stores with sc0, loads with sc1. Modes 1 and 3..5 are meant
+// for a and b on one XCD.
+__device__ __forceinline__ uint32_t pp_ld(const uint32_t* p, int mode) {
+  if (mode == 0) return __hip_atomic_load(const_cast<uint32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc((void*)p, (short)0, 64, 0x00020000);
+  if (mode == 1 || mode == 4 || mode == 5) return __builtin_amdgcn_raw_buffer_load_b32(r, 0, 0, 1);
+  if (mode == 3) {
+    asm volatile("buffer_inv sc0" ::: "memory");
+    return __builtin_amdgcn_raw_buffer_load_b32(r, 0, 0, 0);
+  }
+  return __builtin_amdgcn_raw_buffer_load_b32(r, 0, 0, 16);
+}
+__device__ __forceinline__ void pp_st(uint32_t* p, uint32_t v, int mode) {
+  if (mode == 0) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); return; }
+  const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc((void*)p, (short)0, 64, 0x00020000);
+  if (mode == 2 || mode == 5) __builtin_amdgcn_raw_buffer_store_b32(v, r, 0, 0, 16);
+  else if (mode == 4 || mode == 6) __builtin_amdgcn_raw_buffer_store_b32(v, r, 0, 0, 1);
+  else __builtin_amdgcn_raw_buffer_store_b32(v, r, 0, 0, 0);
+}
+__global__ void fxp_pingpong_kernel(uint32_t* flag, int a, int b, uint32_t rounds, int mode, const uint8_t* load,
+                                    uint64_t load_bytes, uint64_t* out) {
   const int blk = blockIdx.x;
   if (blk == a || blk == b) {
     if (threadIdx.x != 0) return;
@@ -209,15 +231,16 @@ __global__ void fxp_pingpong_kernel(uint32_t* flag, int a, int b, uint32_t round
     bool ok = true;
     for (uint32_t i = 1; i <= rounds && ok; ++i) {
       if (blk == a) {
-        __hip_atomic_store(&flag[0], i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        while (__hip_atomic_load(&flag[32], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != i)
+        pp_st(&flag[0], i, mode);
+        while (pp_ld(&flag[32], mode) != i)
           if (__builtin_amdgcn_s_memrealtime() - t0 > PROBE_LIMIT) { ok = false; break; }
       } else {
-        while (__hip_atomic_load(&flag[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != i)
+        while (pp_ld(&flag[0], mode) != i)
           if (__builtin_amdgcn_s_memrealtime() - t0 > PROBE_LIMIT) { ok = false; break; }
-        __hip_atomic_store(&flag[32], i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        pp_st(&flag[32], i, mode);
       }
     }
+    out[blk == a ? 3 : 4] = xcc_id();
     if (blk == a) {
       out[0] = __builtin_amdgcn_s_memrealtime() - t0;
       out[1] = ok ? 1 : 0;
@@ -287,6 +310,77 @@ __global__ void fxp_clock_kernel(int iters, const uint8_t* load, uint64_t load_b
       out[2] = __float_as_uint(a);
       __hip_atomic_store(done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
+    return;
+  }
+  if (!load) return;
+  const uint64_t per = load_bytes / gridDim.x;
+  const uint8_t* base = load + (uint64_t)blockIdx.x * per;
+  const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+  uint32_t acc = 0;
+  for (int rep = 0; rep < 1000; ++rep) {
+    for (uint64_t off = threadIdx.x * 16; off + 16 * 8 * blockDim.x <= per; off += 16 * 8 * blockDim.x) {
+      u32x4p v[8];
+#pragma unroll
+      for (int d = 0; d < 8; ++d) v[d] = __builtin_nontemporal_load((const u32x4p*)(base + off + (uint64_t)d * 16 * blockDim.x));
+#pragma unroll
+      for (int d = 0; d < 8; ++d) acc += v[d].x;
+    }
+    if (__hip_atomic_load(done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ||
+        __builtin_amdgcn_s_memrealtime() - t0 > PROBE_LIMIT)
+      break;
+  }
+  if (acc == 0x12345678u) out[3] = acc;
+}
+
+// ---- VALU issue rate of FMA chains, one wave per SIMD (256 threads, one workgroup): 1024 v_fmac_f32
+// per lane as one dependent chain, or as 2 / 4 / 8 independent chains interleaved instruction by
+// instruction (each chain itself dependent). out[v] = core cycles (s_memtime) of variant v on wave 0.
+__global__ void __launch_bounds__(256) fxp_valu_kernel(uint64_t* out, float* sink) {
+  float a0 = (float)threadIdx.x, a1 = a0 + 1.0f, a2 = a0 + 2.0f, a3 = a0 + 3.0f, a4 = a0 + 4.0f, a5 = a0 + 5.0f,
+        a6 = a0 + 6.0f, a7 = a0 + 7.0f;
+  const float b = 1.0000001f, c = 0.5f;
+  uint64_t t[5];
+  __syncthreads();
+  t[0] = __builtin_amdgcn_s_memtime();
+  asm volatile(".rept 1024\n v_fmac_f32 %0, %1, %2\n .endr" : "+v"(a0) : "v"(b), "v"(c));
+  t[1] = __builtin_amdgcn_s_memtime();
+  asm volatile(".rept 512\n v_fmac_f32 %0, %2, %3\n v_fmac_f32 %1, %2, %3\n .endr" : "+v"(a0), "+v"(a1) : "v"(b), "v"(c));
+  t[2] = __builtin_amdgcn_s_memtime();
+  asm volatile(".rept 256\n v_fmac_f32 %0, %4, %5\n v_fmac_f32 %1, %4, %5\n v_fmac_f32 %2, %4, %5\n v_fmac_f32 %3, %4, %5\n .endr"
+               : "+v"(a0), "+v"(a1), "+v"(a2), "+v"(a3) : "v"(b), "v"(c));
+  t[3] = __builtin_amdgcn_s_memtime();
+  asm volatile(".rept 128\n v_fmac_f32 %0, %8, %9\n v_fmac_f32 %1, %8, %9\n v_fmac_f32 %2, %8, %9\n v_fmac_f32 %3, %8, %9\n"
+               " v_fmac_f32 %4, %8, %9\n v_fmac_f32 %5, %8, %9\n v_fmac_f32 %6, %8, %9\n v_fmac_f32 %7, %8, %9\n .endr"
+               : "+v"(a0), "+v"(a1), "+v"(a2), "+v"(a3), "+v"(a4), "+v"(a5), "+v"(a6), "+v"(a7) : "v"(b), "v"(c));
+  t[4] = __builtin_amdgcn_s_memtime();
+  if (threadIdx.x == 0)
+    for (int v = 0; v < 4; ++v) out[v] = t[v + 1] - t[v];
+  sink[threadIdx.x] = a0 + a1 + a2 + a3 + a4 + a5 + a6 + a7;
+}
+
+// ---- instruction fetch: block 0 (256 threads, one wave per SIMD) runs a straight-line block of
+// 4096 v_fmac_f32 in the 8-byte encoding (32 KiB of code) twice; the first pass fetches the code
+// (cold), the second finds it in the instruction cache. out[0], out[1] = core cycles of the two
+// passes on wave 0. The other blocks stream-read `load` meanwhile (if non-null), as in the clock probe.
+__global__ void __launch_bounds__(256) fxp_icache_kernel(const uint8_t* load, uint64_t load_bytes, uint32_t* done,
+                                                         uint64_t* out, float* sink) {
+  if (blockIdx.x == 0) {
+    float a = (float)threadIdx.x;
+    const float b = 1.0000001f, c = 0.5f;
+    uint64_t t[3];
+    __syncthreads();
+#pragma unroll 1
+    for (int pass = 0; pass < 2; ++pass) {
+      t[pass] = __builtin_amdgcn_s_memtime();
+      asm volatile(".rept 4096\n v_fmac_f32_e64 %0, %1, %2\n .endr" : "+v"(a) : "v"(b), "v"(c));
+    }
+    t[2] = __builtin_amdgcn_s_memtime();
+    if (threadIdx.x == 0) {
+      out[0] = t[1] - t[0];
+      out[1] = t[2] - t[1];
+      __hip_atomic_store(done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    sink[threadIdx.x] = a;
     return;
   }
   if (!load) return;
@@ -417,7 +511,8 @@ int fxp_chase(const uint32_t* idx, uint32_t hops, int mode, const void* load, ui
   return e;
 }
 
-int fxp_pingpong(int a, int b, uint32_t rounds, const void* load, uint64_t load_bytes, int blocks, uint64_t* out_host) {
+int fxp_pingpong(int a, int b, uint32_t rounds, int mode, const void* load, uint64_t load_bytes, int blocks,
+                 uint64_t* out_host) {
   uint32_t* flag = nullptr;
   uint64_t* out = nullptr;
   hipError_t e;
@@ -425,13 +520,48 @@ int fxp_pingpong(int a, int b, uint32_t rounds, const void* load, uint64_t load_
   if ((e = hipMalloc(&out, 64)) != hipSuccess) return e;
   (void)hipMemset(flag, 0, 1024);
   (void)hipMemset(out, 0, 64);
-  void* args[] = {&flag, &a, &b, &rounds, (void*)&load, &load_bytes, &out};
+  void* args[] = {&flag, &a, &b, &rounds, &mode, (void*)&load, &load_bytes, &out};
   if ((e = hipLaunchCooperativeKernel((const void*)fxp_pingpong_kernel, dim3(blocks), dim3(256), args, 0, 0)) != hipSuccess)
     return e;
   if ((e = hipDeviceSynchronize()) != hipSuccess) return e;
-  e = hipMemcpy(out_host, out, 24, hipMemcpyDeviceToHost);
+  e = hipMemcpy(out_host, out, 40, hipMemcpyDeviceToHost);
   (void)hipFree(flag);
   (void)hipFree(out);
+  return e;
+}
+
+int fxp_icache(const void* load, uint64_t load_bytes, uint64_t* out_host) {
+  uint64_t* out = nullptr;
+  uint32_t* done = nullptr;
+  float* sink = nullptr;
+  hipError_t e;
+  if ((e = hipMalloc(&out, 64)) != hipSuccess) return e;
+  if ((e = hipMalloc(&done, 256)) != hipSuccess) return e;
+  if ((e = hipMalloc(&sink, 1024)) != hipSuccess) return e;
+  (void)hipMemset(done, 0, 256);
+  void* args[] = {(void*)&load, &load_bytes, &done, &out, &sink};
+  if ((e = hipLaunchCooperativeKernel((const void*)fxp_icache_kernel, dim3(256), dim3(256), args, 0, 0)) != hipSuccess)
+    return e;
+  if ((e = hipDeviceSynchronize()) != hipSuccess) return e;
+  e = hipMemcpy(out_host, out, 16, hipMemcpyDeviceToHost);
+  (void)hipFree(out);
+  (void)hipFree(done);
+  (void)hipFree(sink);
+  return e;
+}
+
+int fxp_valu(uint64_t* out_host) {
+  uint64_t* out = nullptr;
+  float* sink = nullptr;
+  hipError_t e;
+  if ((e = hipMalloc(&out, 64)) != hipSuccess) return e;
+  if ((e = hipMalloc(&sink, 1024)) != hipSuccess) return e;
+  hipLaunchKernelGGL(fxp_valu_kernel, dim3(1), dim3(256), 0, 0, out, sink);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  if ((e = hipDeviceSynchronize()) != hipSuccess) return e;
+  e = hipMemcpy(out_host, out, 32, hipMemcpyDeviceToHost);
+  (void)hipFree(out);
+  (void)hipFree(sink);
   return e;
 }
 

@@ -400,6 +400,12 @@ static int check_stage(fx_ctx* c, const fx_stage& s, int idx, int n_total) {
     if (s.src[k] < -n_total || s.src[k] >= n_total) return bad("packet source out of range");
   if ((s.flags & FX_F_MFMA) && s.op != FX_OP_MLA_ATTEND && s.op != FX_OP_MLA_MERGE_UV)
     return bad("FX_F_MFMA marks the attention and its merge only");
+  if ((s.flags & FX_F_XLOCAL) && s.op != FX_OP_MLA_PREP) return bad("FX_F_XLOCAL marks the MLA prep only");
+  if ((s.flags & FX_F_XCD) && s.op != FX_OP_MLA_ATTEND && s.op != FX_OP_MLA_MERGE_UV)
+    return bad("FX_F_XCD marks the attention and its merge only");
+  if ((s.flags & FX_F_XCD) && (s.flags & FX_F_MFMA)) return bad("FX_F_XCD and FX_F_MFMA exclude each other");
+  if ((s.flags & FX_F_SKIP_XCD) && (s.op != FX_OP_GEMV || (s.flags & FX_F_ARGMAX)))
+    return bad("FX_F_SKIP_XCD marks a GEMV without argmax only");
   if (s.flags & FX_F_FP8) {
     const bool head = s.op == FX_OP_GEMV && (s.flags & FX_F_ARGMAX) && s.in_kind == FX_IN_VEC;
     if (s.op != FX_OP_MOE_W13 && s.op != FX_OP_MOE_W2 && !head)
@@ -440,6 +446,11 @@ static int check_stage(fx_ctx* c, const fx_stage& s, int idx, int n_total) {
       if (s.op == FX_OP_MLA_MERGE_UV) {
         if (!s.aux[6] || s.split <= 0) return bad("merge pointers");
         if (s.n_splits * 4 > 37 * 1024) return bad("too many splits for the merge table");
+        if (s.flags & FX_F_XCD) {
+          if (!s.aux[0] || !s.aux[1] || !s.aux[2] || !s.aux[3] || !s.aux[5]) return bad("single-XCD attention pointers");
+          if (s.split % 32 || s.n_splits <= 0 || s.prow < s.d_c + 1 || s.prow % 4) return bad("attend splits");
+          if ((long long)s.n_splits * s.split < s.s_max) return bad("splits do not cover s_max");
+        }
       }
       break;
     case FX_OP_MOE_ROUTER:
@@ -666,8 +677,8 @@ int fx_mla_attend_merge_noalloc(fx_ctx* c, const fx_stage* attend, const fx_stag
   if (!c->scratch) return fail(c, FX_E_STATE, "the context has no scratch address");
   if (attend->op != FX_OP_MLA_ATTEND || merge->op != FX_OP_MLA_MERGE_UV)
     return fail(c, FX_E_ARG, "fx_mla_attend_merge_noalloc takes an MLA_ATTEND stage and an MLA_MERGE_UV stage");
-  if ((attend->flags & FX_F_MFMA) != (merge->flags & FX_F_MFMA))
-    return fail(c, FX_E_ARG, "the attend and merge stages must use the same attention kernel (FX_F_MFMA)");
+  if ((attend->flags & (FX_F_MFMA | FX_F_XCD)) != (merge->flags & (FX_F_MFMA | FX_F_XCD)))
+    return fail(c, FX_E_ARG, "the attend and merge stages must use the same attention kernel (FX_F_MFMA, FX_F_XCD)");
   if (attend->n_splits <= 0 || attend->n_splits > FX_NOALLOC_MAX_SPLITS || merge->n_splits != attend->n_splits ||
       merge->split != attend->split)
     return fail(c, FX_E_ARG, "n_splits must be in [1, " + std::to_string(FX_NOALLOC_MAX_SPLITS) +
@@ -682,7 +693,10 @@ int fx_mla_attend_merge_noalloc(fx_ctx* c, const fx_stage* attend, const fx_stag
   a.aux[6] = done;
   m.x = part;
   m.aux[6] = done;
-  m.src[0] = sidx;
+  // the merge waits for the attention's done packets; the single-XCD merge runs the attention itself
+  // and waits for the attention's inputs
+  const bool xcd = (merge->flags & FX_F_XCD) != 0;
+  m.src[0] = xcd ? attend->src[0] : sidx;
   int r = check_stage(c, a, 0, 1 << 20);
   if (r) return r;
   r = check_stage(c, m, 1, 1 << 20);
@@ -696,8 +710,9 @@ int fx_mla_attend_merge_noalloc(fx_ctx* c, const fx_stage* attend, const fx_stag
   int32_t n_prompt = 1 << 30, sidx_m = sidx + 1;
   int64_t* no_tokens = nullptr;
   void* args_a[] = {(void*)&a, &step, &n_prompt, &tbase, &sidx, &no_tokens, &c->err_flag};
-  HIPCHK(c, hipLaunchCooperativeKernel((const void*)fx_stage_kernel, dim3(FX_BLOCKS), dim3(FX_THREADS), args_a,
-                                       FX_LDS_BYTES, s));
+  if (!xcd)
+    HIPCHK(c, hipLaunchCooperativeKernel((const void*)fx_stage_kernel, dim3(FX_BLOCKS), dim3(FX_THREADS), args_a,
+                                         FX_LDS_BYTES, s));
   void* args_m[] = {(void*)&m, &step, &n_prompt, &tbase, &sidx_m, &no_tokens, &c->err_flag};
   HIPCHK(c, hipLaunchCooperativeKernel((const void*)fx_stage_kernel, dim3(FX_BLOCKS), dim3(FX_THREADS), args_m,
                                        FX_LDS_BYTES, s));

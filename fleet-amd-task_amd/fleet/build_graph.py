@@ -50,6 +50,7 @@ def compile_stages(plan, host):
     reads = []          # per stage: [(src slot, tensor name)]
     pend_embed = None
     pend_router = None
+    pend_attend = None   # the attention call whose work the next merge stage takes (attn "xcd")
     B = lambda n: host[n].ptr if n else 0
 
     def add(st, label, ins):
@@ -115,6 +116,9 @@ def compile_stages(plan, host):
                     flags |= R.FX_F_RESIDUAL
                     st.res = B(a["residual"])
                     ins.append((2, a["residual"]))
+            if plan.attn == "xcd" and a["input"] == "attn":
+                # o_proj right after the single-XCD attention: XCD 7's workers take no rows
+                flags |= R.FX_F_SKIP_XCD
             st.flags = flags
             add(st, lab, ins)
             continue
@@ -124,6 +128,9 @@ def compile_stages(plan, host):
                         x=B(a["qkva"]), w=B(a["w_uk"]), w_norm=B(a["w_kv_norm"]), out=B(a["ql_nope"]),
                         aux={0: B(a["c_kv"]), 1: B(a["k_pe"]), 2: B(a["q_pe"]), 3: B(a["cos"]), 4: B(a["sin"]),
                              5: B(a["crow"])}, **common)
+            if plan.attn == "valu":
+                # the VALU attention reads the XCD's own heads: prep's packets stay in the XCD
+                st.flags |= R.FX_F_XLOCAL
             ins = [(0, a["qkva"])]
         elif m == "mla_attend_layer":
             st = _stage(op=R.FX_OP_MLA_ATTEND, n_rows=d.NH, d_c=d.D_C, d_r=d.D_R, d_n=d.D_N, split=a["split"],
@@ -133,14 +140,30 @@ def compile_stages(plan, host):
                         **common)
             if plan.attn == "mfma":
                 st.flags |= R.FX_F_MFMA
+            if plan.attn == "xcd":
+                # the attention runs inside the merge stage; this stage stays as a (no-op) marker
+                st.flags |= R.FX_F_XCD
+                pend_attend = a
             ins = [(0, a["ql_nope"])]
         elif m == "mla_merge_uv_layer":
             st = _stage(op=R.FX_OP_MLA_MERGE_UV, n_rows=d.NH, d_c=d.D_C, d_r=d.D_R, d_n=d.D_V, split=a["split"],
                         n_splits=a["n_splits"], prow=G.partials_row(d.D_C), x=B(a["input"]), w=B(a["w_uv"]),
                         out=B(a["output"]), aux={4: B(a.get("o_merged")), 6: B(a["done"])}, **common)
+            ins = [(0, a["done"])]
             if plan.attn == "mfma":
                 st.flags |= R.FX_F_MFMA
-            ins = [(0, a["done"])]
+            if plan.attn == "xcd":
+                # the attention and the merge on one XCD: the attention's operands in the spare fields
+                att = pend_attend
+                assert att is not None and att["partials"] == a["input"] and att["done"] == a["done"], \
+                    "the merge must follow its attention"
+                st.flags |= R.FX_F_XCD
+                st.s_max = plan.s_max
+                st.scale = att["softmax_scale"]
+                for k, name in ((0, "c_kv"), (1, "k_pe"), (2, "q_pe"), (3, "ql_nope"), (5, "crow")):
+                    st.aux[k] = B(att[name])
+                pend_attend = None
+                ins = [(0, att["ql_nope"])]
         elif m == "gang_linear_silu_layer":
             st = _stage(op=R.FX_OP_DENSE_GU, n_rows=d.I_DENSE, k=d.H, x=B(a["input"]), w_norm=B(a["w_norm"]),
                         w=B(a["weight"]), out=B(a["output"]), aux={6: B(a.get("h"))}, **common)

@@ -147,15 +147,23 @@ def splits_for(s_max, split=SPLIT, n_splits=None):
     return split, n_splits
 
 
+def default_attn(s_max):
+    """The attention of a plan whose caller names none: the matrix-core attention spread over all
+    workers. (The single-XCD form keeps the attention's exchanges in one XCD's L2 but gives each of
+    its 32 workers a whole head's merge and 64 W_uv rows; measured at ctx 1024 on MI355X it is
+    ~80 us/token slower, so it is not a default.)"""
+    return "mfma"
+
+
 def default_splits(s_max, attn="mfma"):
     """(split, n_splits) of the decode plan.
-    valu: the fewest 32-position tiles per split that keep every split on its own worker of an XCD
-    (at most 32 splits), so the attention runs in one round and the merge reads at most 32 partials
-    per head.
+    valu, xcd: the fewest 32-position tiles per split that keep every split on its own worker of an
+    XCD (at most 32 splits), so the attention runs in one round and the merge reads at most 32
+    partials per head.
     mfma: one split per worker and every head per split, so the splits are short: 32 positions up
     to 32 splits, then as many positions as keep the split count at most 64 (the merge reads every
     live split's partial for its head)."""
-    if attn == "valu":
+    if attn in ("valu", "xcd"):
         return splits_for(s_max, n_splits=XWORKERS)
     if -(-s_max // SPLIT) <= 32:
         return splits_for(s_max, SPLIT)
@@ -164,13 +172,15 @@ def default_splits(s_max, attn="mfma"):
 
 def build_plan(dims: Dims = REAL_DIMS, s_max: int = 1056, layers: int = 27, head: bool = True, split: int = None,
                n_splits: int = None, iters_cap: int = 32, softmax_scale: float = SOFTMAX_SCALE,
-               eps: float = RMS_EPS, fp8_experts: bool = False, fp8_head: bool = False, attn: str = "mfma") -> Plan:
+               eps: float = RMS_EPS, fp8_experts: bool = False, fp8_head: bool = False, attn: str = None) -> Plan:
     """split / n_splits: the attention split (positions) or split count; neither: default_splits.
-    attn: "mfma" (the matrix-core attention: splits over all workers, every head per split) or
-    "valu" (heads over XCDs, score chains on the vector ALUs)."""
+    attn: "mfma" (the matrix-core attention: splits over all workers, every head per split), "xcd"
+    (the same attention and its merge on the 32 workers of one XCD, partials in its L2), "valu"
+    (heads over XCDs, score chains on the vector ALUs), or None: default_attn(s_max)."""
     d = dims
     assert 1 <= layers <= d.L
-    assert attn in ("mfma", "valu"), attn
+    attn = default_attn(s_max) if attn is None else attn
+    assert attn in ("mfma", "valu", "xcd"), attn
     split, n_splits = splits_for(s_max, split, n_splits) if (split or n_splits) else default_splits(s_max, attn)
     p = Plan(d, s_max, layers, head, split, n_splits)
     p.attn = attn

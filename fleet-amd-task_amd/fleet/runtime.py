@@ -26,6 +26,9 @@ FX_IN_VEC, FX_IN_EMBED = 0, 1
 FX_F_NORM, FX_F_RESIDUAL, FX_F_ARGMAX, FX_F_HEAD, FX_F_OUT_LL, FX_F_RES_EMBED, FX_F_ROUTER = 1, 2, 8, 16, 32, 64, 128
 FX_F_FP8 = 256
 FX_F_MFMA = 512
+FX_F_XLOCAL = 1024
+FX_F_XCD = 2048
+FX_F_SKIP_XCD = 4096
 FX_MAX_ITERS, FX_MAX_MARKS, FX_PROF_SLOTS = 65536, 256, 8
 FX_ABI_VERSION = 4
 WORKERS = 256          # one worker workgroup per CU

@@ -95,7 +95,8 @@ def main():
     ap.add_argument("--json", default=None)
     ap.add_argument("--n-splits", type=int, default=None, help="attention split count (default: the plan's own)")
     ap.add_argument("--split", type=int, default=None, help="attention split length (a multiple of 32)")
-    ap.add_argument("--attn", choices=("mfma", "valu"), default="mfma", help="attention kernel")
+    ap.add_argument("--attn", choices=("mfma", "xcd", "valu"), default=None,
+                    help="attention kernel (default: the plan's own choice)")
     ap.add_argument("--fp8-experts", action="store_true", help="FP8 expert weights (pack_weights.quantize_experts)")
     args = ap.parse_args()
     d = P.REAL_DIMS

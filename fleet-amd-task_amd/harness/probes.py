@@ -30,8 +30,11 @@ def probe_lib():
     L.fxp_stream.argtypes = [vp, u64, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.POINTER(u64),
                              ctypes.POINTER(ctypes.c_float)]
     L.fxp_chase.argtypes = [vp, u32, ctypes.c_int, vp, u64, ctypes.c_int, ctypes.POINTER(u64)]
-    L.fxp_pingpong.argtypes = [ctypes.c_int, ctypes.c_int, u32, vp, u64, ctypes.c_int, ctypes.POINTER(u64)]
+    L.fxp_pingpong.argtypes = [ctypes.c_int, ctypes.c_int, u32, ctypes.c_int, vp, u64, ctypes.c_int,
+                               ctypes.POINTER(u64)]
     L.fxp_lanes.argtypes = [ctypes.POINTER(ctypes.c_float)]
+    L.fxp_valu.argtypes = [ctypes.POINTER(u64)]
+    L.fxp_icache.argtypes = [vp, u64, ctypes.POINTER(u64)]
     L.fxp_clock.argtypes = [ctypes.c_int, vp, u64, ctypes.POINTER(u64)]
     L.fxp_lds_dma.argtypes = [ctypes.POINTER(u32)]
     L.fxp_fp8.argtypes = [ctypes.POINTER(ctypes.c_float)]
@@ -54,6 +57,8 @@ def main():
     ap.add_argument("--lanes-only", action="store_true")
     ap.add_argument("--stream-only", action="store_true")
     ap.add_argument("--clock", action="store_true")
+    ap.add_argument("--pingpong-only", action="store_true", help="only the flag round trips")
+    ap.add_argument("--valu", action="store_true", help="only the VALU issue rate of FMA chains")
     ap.add_argument("--reuse", action="store_true",
                     help="cold (first touch) against warm (re-read) streams, register and direct-to-LDS loads")
     args = ap.parse_args()
@@ -80,6 +85,22 @@ def main():
     if args.lanes_only:
         return
     lines = []
+    if args.valu:
+        out = (ctypes.c_uint64 * 4)()
+        for rep in range(2):
+            assert L.fxp_valu(out) == 0
+        for v, chains in enumerate((1, 2, 4, 8)):
+            print(f"VALU: 1024 v_fmac_f32 per lane as {chains} interleaved dependent chain(s), one wave per SIMD: "
+                  f"{out[v]} core cycles, {out[v] / 1024:.2f} cycles per instruction", flush=True)
+        big = rt.alloc((2 << 30,), "u8")
+        oc = (ctypes.c_uint64 * 2)()
+        for rep, load in enumerate((False, False, True, True)):
+            assert L.fxp_icache(ctypes.c_void_p(big.ptr) if load else None, big.nbytes, oc) == 0
+            print(f"instruction fetch ({'under stream' if load else 'idle'}, launch {rep}): 4096 x 8-byte v_fmac_f32 "
+                  f"straight-line, cold pass {oc[0]} cycles ({oc[0] / 4096:.2f}/instr), warm pass {oc[1]} cycles "
+                  f"({oc[1] / 4096:.2f}/instr)", flush=True)
+        rt.close()
+        return
     if args.clock:
         big = rt.alloc((2 << 30,), "u8")
         out = (ctypes.c_uint64 * 3)()
@@ -99,6 +120,12 @@ def main():
     big = rt.alloc((2 << 30,), "u8")
     rt.fill_u16(big, 0x3F80, n=big.nbytes // 2)
     rt.synchronize()
+    if args.pingpong_only:
+        pingpong(L, big, say)
+        if args.out:
+            Path(args.out).write_text("\n".join(lines) + "\n")
+        rt.close()
+        return
     if args.reuse:
         # global_load_lds with 16 bytes per lane: lane l's bytes land at the LDS base + 16 l
         got = (ctypes.c_uint32 * 512)()
@@ -163,7 +190,14 @@ def main():
         if args.out:
             Path(args.out).write_text("\n".join(lines) + "\n")
         return
-    # ---- chase
+    chase(rt, L, big, say)
+    pingpong(L, big, say)
+    if args.out:
+        Path(args.out).write_text("\n".join(lines) + "\n")
+    rt.close()
+
+
+def chase(rt, L, big, say):
     say("\n## dependent-load latency (one lane, pointer chase, stride 256 B)\n")
     say("| footprint | policy | load | ns/load |")
     say("|---|---|---|---|")
@@ -187,20 +221,27 @@ def main():
                 assert rc == 0, rc
                 say(f"| {name} | {pol} | {'stream' if load else 'idle'} | {out[0] * TICK_NS / hops:.0f} |")
         buf.free()
-    # ---- ping-pong
-    say("\n## flag round trip between two workgroups (agent-scope relaxed store / load)\n")
-    say("| a (XCD) | b (XCD) | load | ns/round trip |")
-    say("|---|---|---|---|")
-    out = (ctypes.c_uint64 * 3)()
+
+
+def pingpong(L, big, say):
+    say("\n## flag round trip between two workgroups\n")
+    say("policy: agent = agent-scope relaxed atomic store / load; sc1 = buffer store / load with sc1 (the decode "
+        "kernel's packets); sc0 = buffer store / load with sc0 (same XCD only; the rest likewise)\n")
+    say("| a (XCD) | b (XCD) | policy | load | ns/round trip |")
+    say("|---|---|---|---|---|")
+    out = (ctypes.c_uint64 * 5)()
     for a, b in ((8, 16), (8, 9), (8, 13)):
-        for load in (False, True):
-            lp = ctypes.c_void_p(big.ptr) if load else None
-            rc = L.fxp_pingpong(a, b, 2000, lp, big.nbytes, 256, out)
-            assert rc == 0 and out[1] == 1, (rc, out[1])
-            say(f"| {a} ({a % 8}) | {b} ({b % 8}) | {'stream' if load else 'idle'} | {out[0] * TICK_NS / 2000:.0f} |")
-    if args.out:
-        Path(args.out).write_text("\n".join(lines) + "\n")
-    rt.close()
+        for mode, pol in ((0, "agent"), (2, "sc1"), (4, "sc0"), (1, "sc0 load, plain store"),
+                          (3, "plain store, L1 invalidate + plain load"), (5, "sc1 store, sc0 load"),
+                          (6, "sc0 store, sc1 load")):
+            if mode in (1, 3, 4, 5) and a % 8 != b % 8:
+                continue
+            for load in (False, True):
+                lp = ctypes.c_void_p(big.ptr) if load else None
+                rc = L.fxp_pingpong(a, b, 2000, mode, lp, big.nbytes, 256, out)
+                assert rc == 0, rc
+                rt_ns = f"{out[0] * TICK_NS / 2000:.0f}" if out[1] == 1 else "no round trip within 1 s"
+                say(f"| {a} ({out[3]}) | {b} ({out[4]}) | {pol} | {'stream' if load else 'idle'} | {rt_ns} |")
 
 
 if __name__ == "__main__":

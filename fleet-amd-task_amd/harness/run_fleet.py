@@ -64,8 +64,9 @@ def build_parser():
     ap.add_argument("--seed", type=int, default=SEED, help="weight and prompt seed")
     ap.add_argument("--split", type=int, default=None, help="attention split length (a multiple of 32)")
     ap.add_argument("--n-splits", type=int, default=None, help="attention split count (default: the plan's own)")
-    ap.add_argument("--attn", choices=("mfma", "valu"), default="mfma",
-                    help="attention kernel: matrix cores over all workers (mfma) or vector-ALU chains per XCD (valu)")
+    ap.add_argument("--attn", choices=("mfma", "xcd", "valu"), default=None,
+                    help="attention kernel: matrix cores over all workers (mfma), matrix cores with the merge on one "
+                         "XCD (xcd), or vector-ALU chains per XCD (valu); default: the plan's own choice")
     ap.add_argument("--out", default=None, help="run directory (default: harness/fleet_out/<name>)")
     ap.add_argument("--event-timing", action="store_true", help="per-stage stamps of the last iteration")
     ap.add_argument("--prefill", choices=("decode", "batched"), default="decode",

@@ -119,6 +119,19 @@ enum fx_op {
                             * waits for workers 0 .. min(live splits, 256) - 1 and runs on workers 128..255,
                             * 8 per head (16 W_uv rows each) */
 
+#define FX_F_XLOCAL 1024u  /* MLA_PREP: every reader of its packets runs on the producing XCD (the VALU
+                            * attention: XCD x owns heads 2x, 2x + 1), so they are stored XCD-local (sc0)
+                            * instead of device-coherent (sc1) */
+#define FX_F_XCD 2048u     /* the single-XCD matrix-core attention. MLA_ATTEND: the stage does nothing.
+                            * MLA_MERGE_UV: the attention of every head and its merge on the 32 workers of
+                            * XCD 7 (split j on rank j % 32, rank r merges head r / 2 and W_uv rows
+                            * 64 (r % 2) ..); partials (x) and done packets (aux6, one per rank) stay in
+                            * that XCD's L2. The attention's operands ride in the merge's spare fields:
+                            * aux3 = ql_nope packets, aux0 c_kv, aux1 k_pe, aux2 q_pe packets, aux5 crow
+                            * packets, scale, s_max; src[0] = their producer */
+#define FX_F_SKIP_XCD 4096u /* GEMV: rows split over the workers of XCDs 0..6 only (XCD 7 runs the
+                            * single-XCD attention just before) */
+
 /* One entry of the task table: one operator of the plan (fleet/graph_plan.py Call). */
 typedef struct fx_stage {
   int32_t op, flags, in_kind;

@@ -80,7 +80,7 @@ def layer_step(cfg, W, cache, cos, sin, x_res, step, l, rec=None):
                                         c.NH, c.D_N, c.D_R, c.D_C, c.eps)
     cache.c_kv[l][step] = c_row
     cache.k_pe[l][step] = k_pe_row
-    attend = O.mla_attend_mfma if c.attn == "mfma" else O.mla_attend
+    attend = O.mla_attend_mfma if c.attn in ("mfma", "xcd") else O.mla_attend
     partials = attend(ql, qp, cache.c_kv[l], cache.k_pe[l], step, c.scale, c.split, c.n_splits)
     attn, obf = O.mla_merge_uv(partials, W[f"W_uv_{l}"], step, c.split)
     x_attn, _ = O.linear(W[f"W_o_{l}"], attn, res=x_res)

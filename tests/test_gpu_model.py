@@ -37,7 +37,7 @@ def _run_model(rt, layers, n_prompt, n_new, s_max, attn, seed=SEED):
     return d, bufs, prompt, plan, runner, cap
 
 
-@pytest.mark.parametrize("attn", ["mfma", "valu"])
+@pytest.mark.parametrize("attn", ["mfma", "xcd", "valu"])
 @pytest.mark.parametrize("layers,n_prompt,n_new", [(2, 40, 4), (3, 70, 3)])
 def test_decode_matches_oracle(rt, layers, n_prompt, n_new, attn):
     s_max = 96
@@ -65,7 +65,7 @@ def test_decode_matches_oracle(rt, layers, n_prompt, n_new, attn):
                 assert rl[i, j].tolist() == r, (i, j, rl[i, j].tolist(), r)
 
 
-@pytest.mark.parametrize("attn", ["mfma", "valu"])
+@pytest.mark.parametrize("attn", ["mfma", "xcd", "valu"])
 def test_last_step_buffers_match_oracle(rt, attn):
     """One decode iteration of a 2-layer model from a seeded random cache (BASELINE config 0's
     setting: 1,024 cached positions ~N(0,1)); every workspace the last layer leaves behind is

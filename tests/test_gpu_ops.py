@@ -248,6 +248,56 @@ def test_mla_attend_merge_uv(rt, attn, s_max, step, split):
     assert mismatch(attn.download(tag=TOUT + 1), e_attn) == 0
 
 
+XCD_POINTS = [(1056, 1023, 32),                     # 32 live splits: one per rank of the XCD
+              (1056, 1040, 32),                     # 33: rank 0 runs two
+              (8192, 4127, 32)]                     # 129: four or five per rank, lse beyond 128 splits
+
+
+@pytest.mark.parametrize("s_max,step,split", ATTEND_POINTS + XCD_POINTS)
+def test_mla_attend_merge_xcd(rt, s_max, step, split):
+    """The single-XCD matrix-core attention and its merge in one stage (FX_F_XCD on the merge): the
+    partials, the done packets of XCD 7's ranks, o_merged and attn, against the oracle's matrix-core
+    attention and merge + W_uv."""
+    print(f"[attend-xcd] s_max={s_max} step={step} split={split}", flush=True)
+    rng = np.random.default_rng(s_max + step + 7)
+    n_splits = -(-s_max // split)
+    live = -(-(step + 1) // split)
+    prow = partials_row(DC)
+    ql, qp = rng_bf16(rng, (NH, DC)), rng_bf16(rng, (NH, DR))
+    ck, kp = rng_bf16(rng, (s_max, DC)), rng_bf16(rng, (s_max, DR))
+    scale = float(np.float32(1 / np.sqrt(192)))
+    ckd, kpd = ck.copy(), kp.copy()
+    ckd[step] = SENT16
+    kpd[step] = SENT16
+    crow = pk(rt, np.tile(np.concatenate([ck[step], kp[step]]), (8, 1)))
+    part = sentinel(rt, (n_splits, NH, prow), "f32")
+    done = pk_out(rt, (8, 32), "pk32")
+    W_uv = rng_bf16(rng, (NH, DN, DC), 0.05)
+    attn = pk_out(rt, (NH * DN,))
+    om = sentinel(rt, (NH, DC), "bf16")
+    st = R.FxStage().set(op=R.FX_OP_MLA_MERGE_UV, flags=R.FX_F_XCD, n_rows=NH, d_c=DC, d_r=DR, d_n=DN, split=split,
+                         n_splits=n_splits, prow=prow, s_max=s_max, scale=scale, x=part.ptr,
+                         w=dev(rt, W_uv, "bf16").ptr, out=attn.ptr,
+                         aux={0: dev(rt, ckd, "bf16").ptr, 1: dev(rt, kpd, "bf16").ptr, 2: pk(rt, qp).ptr,
+                              3: pk(rt, ql).ptr, 4: om.ptr, 5: crow.ptr, 6: done.ptr}, src=[SRC, 0, 0, 0])
+    rt.run_stage(st, step=step, tbase=TB, sidx=SIDX)
+    exp = O.mla_attend_mfma(ql, qp, ck, kp, step, scale, split=split, n_splits=n_splits)
+    got = part.download()
+    bad = mismatch(got[:live, :, :DC + 1], exp[:live, :, :DC + 1])
+    if bad:
+        d = np.argwhere(got[:live, :, :DC + 1].view(np.uint32) != exp[:live, :, :DC + 1].view(np.uint32))
+        print(f"[attend-xcd] {bad} partials differ, first (split, head, col) {d[:6].tolist()}", flush=True)
+    assert bad == 0
+    # one done packet per rank that owned a live split (split j on rank j % 32), split counts summing to live
+    nown = min(live, 32)
+    vals, tags = R.unpack_packets(done.download_raw(), "pk32")
+    assert (tags[:nown] == TOUT).all() and (tags[nown:] == 0).all()
+    assert int(vals[:nown].view(np.uint32).sum()) == live
+    e_attn, e_obf = O.mla_merge_uv(exp, W_uv, step, split=split)
+    assert mismatch(om.download(), e_obf) == 0
+    assert mismatch(attn.download(tag=TOUT), e_attn) == 0
+
+
 def test_router_experts_combine(rt):
     """router (row e on worker e) -> w13 + SiLU (slot = XCD) -> w2 + combine (8 rows per worker, all
     slots), against the oracle's moe_router, moe_w13_silu, moe_w2 and moe_combine on the selected

@@ -42,9 +42,11 @@ def test_plan_counts_and_chain():
     assert s["ops"] == 1 + 27 * 5 + 2 + 26 * 4 + 2
     assert p.chain_violations() == []
     # defaults: the matrix-core attention takes 32-position splits (one per worker) up to 32 splits;
-    # the vector-ALU attention at most 32 splits (one per worker of an XCD)
+    # the vector-ALU and single-XCD attentions at most 32 splits (one per worker of an XCD)
     assert (p.attn, p.split, p.n_splits) == ("mfma", 32, 33)
     assert (G.build_plan(attn="valu").split, G.build_plan(attn="valu").n_splits) == (64, 17)
+    xc = G.build_plan(attn="xcd")
+    assert (xc.attn, xc.split, xc.n_splits) == ("xcd", 64, 17)
     assert G.default_splits(16416) == (288, 57)
     assert (G.build_plan(split=32).split, G.build_plan(split=32).n_splits) == (32, 33)
     t = G.build_plan().truncate("L1.o_proj")

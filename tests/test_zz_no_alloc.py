@@ -50,12 +50,16 @@ def _stages(inp, s_max, split, flags, part, done, attn, om):
     m = R.FxStage().set(op=R.FX_OP_MLA_MERGE_UV, flags=flags, n_rows=NH, d_c=DC, d_r=DR, d_n=DN, split=split,
                         n_splits=inp["n_splits"], prow=prow, x=part, w=inp["W"].ptr, out=attn.ptr,
                         aux={4: om.ptr, 6: done}, src=[SIDX, 0, 0, 0])
+    if flags & R.FX_F_XCD:
+        # the single-XCD merge runs the attention itself: its operands, and the prep as its source
+        m.set(s_max=s_max, scale=a.scale, aux={0: inp["ck"].ptr, 1: inp["kp"].ptr, 2: inp["qp"].ptr, 3: inp["q"].ptr,
+                                               4: om.ptr, 5: inp["crow"].ptr, 6: done}, src=[SRC, 0, 0, 0])
     return a, m
 
 
-@pytest.mark.parametrize("attn", ["mfma", "valu"])
+@pytest.mark.parametrize("attn", ["mfma", "xcd", "valu"])
 def test_noalloc_attention_matches_the_kernel_suite_path(rt, attn):
-    flags = R.FX_F_MFMA if attn == "mfma" else 0
+    flags = {"mfma": R.FX_F_MFMA, "xcd": R.FX_F_XCD, "valu": 0}[attn]
     keep = []
     # two calls in a row on the same GPU: a large one, then a smaller one
     for s_max, step, split, seed in ((1056, 1023, 32, 1), (300, 40, 32, 2)):
