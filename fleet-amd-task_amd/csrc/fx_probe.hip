@@ -403,6 +403,16 @@ __global__ void __launch_bounds__(256) fxp_icache_kernel(const uint8_t* load, ui
   if (acc == 0x12345678u) out[3] = acc;
 }
 
+// ---- v_dot2c_f32_bf16 on given operands: d[i] = dot2(a[i], b[i]) + c[i], a and b two bf16 each
+// (low half = element 0); the host compares the results with candidate rounding models.
+typedef __bf16 fxp_bf16x2 __attribute__((ext_vector_type(2)));
+__global__ void fxp_dot2_kernel(const uint32_t* a, const uint32_t* b, const float* c, float* d, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  d[i] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(fxp_bf16x2, a[i]), __builtin_bit_cast(fxp_bf16x2, b[i]), c[i],
+                                         false);
+}
+
 // ---- direct-to-LDS layout: one wave loads 2 KiB of src (u32 index values) with two 16-byte
 // global_load_lds at LDS offsets 0 and 1024 (the second from src + 1024 + 16 * (63 - lane), lanes
 // reversed), then copies the 2 KiB of LDS to dst as they lie
@@ -527,6 +537,29 @@ int fxp_pingpong(int a, int b, uint32_t rounds, int mode, const void* load, uint
   e = hipMemcpy(out_host, out, 40, hipMemcpyDeviceToHost);
   (void)hipFree(flag);
   (void)hipFree(out);
+  return e;
+}
+
+int fxp_dot2(const uint32_t* a_host, const uint32_t* b_host, const float* c_host, float* d_host, int n) {
+  uint32_t *a = nullptr, *b = nullptr;
+  float *c = nullptr, *d = nullptr;
+  hipError_t e;
+  const size_t by = (size_t)n * 4;
+  if ((e = hipMalloc(&a, by)) != hipSuccess) return e;
+  if ((e = hipMalloc(&b, by)) != hipSuccess) return e;
+  if ((e = hipMalloc(&c, by)) != hipSuccess) return e;
+  if ((e = hipMalloc(&d, by)) != hipSuccess) return e;
+  if ((e = hipMemcpy(a, a_host, by, hipMemcpyHostToDevice)) != hipSuccess) return e;
+  if ((e = hipMemcpy(b, b_host, by, hipMemcpyHostToDevice)) != hipSuccess) return e;
+  if ((e = hipMemcpy(c, c_host, by, hipMemcpyHostToDevice)) != hipSuccess) return e;
+  hipLaunchKernelGGL(fxp_dot2_kernel, dim3((n + 255) / 256), dim3(256), 0, 0, a, b, c, d, n);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  if ((e = hipDeviceSynchronize()) != hipSuccess) return e;
+  e = hipMemcpy(d_host, d, by, hipMemcpyDeviceToHost);
+  (void)hipFree(a);
+  (void)hipFree(b);
+  (void)hipFree(c);
+  (void)hipFree(d);
   return e;
 }
 

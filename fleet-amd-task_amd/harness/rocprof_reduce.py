@@ -8,6 +8,7 @@ and its `counters_collection` view (one row per dispatch and counter).
 
   trace    kernel-trace summary: calls, total / average / min / max duration per kernel, and the
            dispatches of --kernel with their durations; with --iters, the duration per iteration
+  counters every counter of the last --kernel dispatch in one or more counter runs
   traffic  HBM bytes per dispatch of --kernel from two counter runs (FETCH_SIZE, then WRITE_SIZE,
            both in KiB per dispatch), each scaled by the same counter on a copy kernel of known size
            (harness/copy_calib.py: every dispatch reads and writes --calib-mib MiB); writes the JSON
@@ -92,6 +93,24 @@ def cmd_trace(a):
         Path(a.json).write_text(json.dumps(out, indent=1) + "\n")
 
 
+def cmd_counters(a):
+    """Every counter of the --kernel dispatch with the largest duration-free index (the last one) in
+    each given database: per-dispatch totals (summed over the counter's instances)."""
+    out = {}
+    for db in a.db:
+        names = [r[0] for r in _rows(db, "select distinct counter_name from counters_collection")]
+        for n in sorted(names):
+            vals = counter_per_dispatch(db, n, kernel=a.kernel)
+            if vals:
+                out[n] = vals[-1]
+    lines = [f"| counter | {a.kernel} (last dispatch) |", "|---|---|"]
+    lines += [f"| {k} | {v:.6g} |" for k, v in out.items()]
+    text = "\n".join(lines)
+    print(text)
+    if a.json:
+        Path(a.json).write_text(json.dumps(out, indent=1) + "\n")
+
+
 def cmd_traffic(a):
     calib_bytes = a.calib_mib * (1 << 20)
     cf = counter_per_dispatch(a.calib_fetch, "FETCH_SIZE", contains=a.calib_kernel)
@@ -140,8 +159,12 @@ def main():
     r.add_argument("--calib-kernel", default="elementwise")
     r.add_argument("--workload", default="bench.py --warmup 0 (configs[3], ctx 1024), timed tokens as one launch")
     r.add_argument("--json", default=None)
+    c = sub.add_parser("counters")
+    c.add_argument("--db", required=True, nargs="+")
+    c.add_argument("--kernel", default="fx_persistent")
+    c.add_argument("--json", default=None)
     a = ap.parse_args()
-    {"trace": cmd_trace, "traffic": cmd_traffic}[a.cmd](a)
+    {"trace": cmd_trace, "traffic": cmd_traffic, "counters": cmd_counters}[a.cmd](a)
 
 
 if __name__ == "__main__":

@@ -49,6 +49,7 @@ def _load():
         "or_round_bf16_array": (None, [_f32p, _u16p, _i64]),
         "or_dot_lanes": (_f, [_u16p, _u16p, _i]),
         "or_mfma_dot32": (_f, [_u16p, _u16p, _i, _f]),
+        "or_dot2": (_f, [ctypes.c_uint16, ctypes.c_uint16, ctypes.c_uint16, ctypes.c_uint16, _f]),
         "or_mfma_cases": (None, [_u16p, _u16p, _f32p, _f32p, _i64]),
         "or_rmsnorm": (None, [_u16p, _u16p, _i, _f, _u16p]),
         "or_rope": (None, [_u16p, _u16p, _u16p, _i, _u16p]),
@@ -160,6 +161,12 @@ def mfma_dot32(a, b, c=0.0):
 def dot_lanes(a, b):
     a, b = _c(a, np.uint16), _c(b, np.uint16)
     return np.float32(lib().or_dot_lanes(a, b, a.size))
+
+
+def dot2(a0, a1, b0, b1, acc=0.0):
+    """gfx950 v_dot2c_f32_bf16: acc + a0 b0 + a1 b1 (bf16 bits) with the instruction's own
+    accumulation (fleet_oracle.c, dot2_hw)."""
+    return np.float32(lib().or_dot2(int(a0), int(a1), int(b0), int(b1), float(acc)))
 
 
 def rmsnorm(x, w, eps=1e-6):
