@@ -632,19 +632,21 @@ __device__ __forceinline__ void merge_head(const void* part, int nh, int h, int 
 
 // FX_OP_MLA_MERGE_UV: ranks 0..15 / 16..31 of XCD x merge head 2x / 2x + 1 (merge_head), then
 // attn[h*d_v + v] = bf16(dot(o, W_uv[h][v])) for 8 rows v each (harness/numpy_ref.py:168-174).
-// With FX_F_MFMA the merge runs on workers 128..255 only, 8 per head (16 W_uv rows each): every
-// merge worker reads all of its head's partials, so fewer workers per head read fewer bytes, and the
-// attention's workers (0 .. live - 1) are not on the merge's critical path while live <= 128.
-#define MERGE_MFMA_FIRST 128
+// With FX_F_MFMA the merge runs on ranks 16..31 of every XCD only (workers 128..255), 8 per head
+// (16 W_uv rows each): ranks 16..23 / 24..31 of XCD x take head 2x / 2x + 1. Every merge worker
+// reads all of its head's partials; the eight readers of a head share one XCD's L2, so HBM sees
+// each partial once, and the attention's workers (0 .. live - 1) are not on the merge's critical
+// path while live <= 128.
+#define MERGE_MFMA_FIRST_RANK 16
 #define MERGE_MFMA_PER_HEAD 8
 __device__ __forceinline__ void op_mla_merge_uv(const fx_stage& s, FxEnv& env) {
   const int nh = s.n_rows, d_c = s.d_c, d_v = s.d_n, prow = s.prow;
   const bool mfma = (s.flags & FX_F_MFMA) != 0;
-  if (mfma && env.worker < MERGE_MFMA_FIRST) return;
-  const int mw = env.worker - MERGE_MFMA_FIRST;
-  const int h = mfma ? mw / MERGE_MFMA_PER_HEAD : env.xcd * MLA_HP + (env.xrank >> 4);
+  if (mfma && env.xrank < MERGE_MFMA_FIRST_RANK) return;
+  const int mr = env.xrank - MERGE_MFMA_FIRST_RANK;
+  const int h = env.xcd * MLA_HP + (mfma ? mr / MERGE_MFMA_PER_HEAD : env.xrank >> 4);
   const int nrows = mfma ? d_v / MERGE_MFMA_PER_HEAD : d_v / 16;   // 16 or 8
-  const int v0 = mfma ? (mw % MERGE_MFMA_PER_HEAD) * nrows : (env.xrank & 15) * nrows;
+  const int v0 = mfma ? (mr % MERGE_MFMA_PER_HEAD) * nrows : (env.xrank & 15) * nrows;
   const int live = (env.step + 1 + s.split - 1) / s.split;
   float* xs = (float*)(env.lds + LDS_XS);
   float* red = (float*)(env.lds + LDS_RED);

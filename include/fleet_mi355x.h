@@ -116,8 +116,9 @@ enum fx_op {
 #define FX_F_MFMA 512u     /* MLA_ATTEND / MLA_MERGE_UV: the matrix-core attention. Split j runs on worker
                             * j % 256 for all heads (tiles of 32 positions; scores and value products on
                             * v_mfma_f32_16x16x32_bf16); done(aux6) holds one packet per worker, the merge
-                            * waits for workers 0 .. min(live splits, 256) - 1 and runs on workers 128..255,
-                            * 8 per head (16 W_uv rows each) */
+                            * waits for workers 0 .. min(live splits, 256) - 1 and runs on ranks 16..31 of
+                            * every XCD (workers 128..255): ranks 16..23 / 24..31 of XCD x take head 2x /
+                            * 2x + 1, 16 W_uv rows each */
 
 #define FX_F_XLOCAL 1024u  /* MLA_PREP: every reader of its packets runs on the producing XCD (the VALU
                             * attention: XCD x owns heads 2x, 2x + 1), so they are stored XCD-local (sc0)
