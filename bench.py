@@ -159,6 +159,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--n-splits", type=int, default=None, help="attention split count (default: the plan's own)")
     ap.add_argument("--split", type=int, default=None, help="attention split length in positions (a multiple of 32)")
+    ap.add_argument("--no-pair", action="store_true",
+                    help="run o_proj and the expert gate|up stage as two operators (no early expert loads)")
     ap.add_argument("--attn", choices=("mfma", "xcd", "valu"), default=None,
                     help="attention kernel: matrix cores over all workers (mfma), matrix cores with the merge on one "
                          "XCD (xcd), or vector-ALU chains per XCD (valu); default: the plan's own choice for the "
@@ -198,7 +200,7 @@ def main():
             P.quantize_head(rt, bufs, d)
         log(f"FP8 experts{' and LM head' if args.fp8_head else ''}: quantized in {time.time() - t0:.1f} s")
     plan_kw = dict(split=args.split, n_splits=args.n_splits, fp8_experts=args.fp8_experts, fp8_head=args.fp8_head,
-                   attn=args.attn)
+                   attn=args.attn, pair=not args.no_pair)
     plan = G.build_plan(d, s_max, d.L, True, **plan_kw)
     meta = B.make_meta(rt, s_max, prompt)
     cap = B.make_capture(rt, plan)
@@ -263,7 +265,7 @@ def main():
                 + ", seeded uniform 1024-token prompt",
         "config": {"workload": "BASELINE configs[3]: DeepSeek-V2-Lite 27 layers, 1024-token prompt (prefill untimed), "
                                "greedy decode at batch 1", "layers": d.L, "batch": 1, "ctx": ctx, "decode_tokens": K,
-                   "splits": plan.n_splits, "split": plan.split, "attn": plan.attn, "seed": args.seed, "fp8_experts": args.fp8_experts,
+                   "splits": plan.n_splits, "split": plan.split, "attn": plan.attn, "pair": plan.pair, "seed": args.seed, "fp8_experts": args.fp8_experts,
                    "fp8_head": args.fp8_head},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBPS, 4),

@@ -298,7 +298,7 @@ __device__ __forceinline__ void op_mla_attend_merge_xcd(const fx_stage& s, FxEnv
   __syncthreads();
   prof_mark(env, 5);
   float* xs = (float*)(env.lds + LDS_XS);
-  merge_head(part, nh, h, s.prow, d_c, live, xs, (float*)(env.lds + LDS_TILE), (float*)(env.lds + LDS_RED));
+  merge_head(part, nh, h, s.prow, d_c, live, xs, (float*)(env.lds + LDS_TILE), (float*)(env.lds + LDS_RED), env);
   if (v0 == 0 && s.aux[4])
     stc4((void*)s.aux[4], (uint32_t)(h * d_c + fx_tid() * 2) * 2, pack2(xs[fx_tid() * 2], xs[fx_tid() * 2 + 1]));
   __syncthreads();

@@ -32,6 +32,10 @@ __device__ __forceinline__ uint32_t tag_out(const FxEnv& e) { return e.tbase + (
 __device__ __forceinline__ void prof_mark(const FxEnv& e, int slot) {
   if (e.pst && fx_tid() == 0) e.pst[slot] = __builtin_amdgcn_s_memrealtime();
 }
+// the same from the calling wave's lane 0 (a stamp taken on a wave other than wave 0)
+__device__ __forceinline__ void prof_mark_wave(const FxEnv& e, int slot) {
+  if (e.pst && lane_id() == 0) e.pst[slot] = __builtin_amdgcn_s_memrealtime();
+}
 
 // LDS layout (bytes)
 #define LDS_XS 0                         // f32 [11264]  GEMV input row

@@ -162,18 +162,19 @@ __device__ __forceinline__ void gemv_prime(TileT& t0, const WT& W, int K, int ng
   if (wave_id() < ngroups) tile_load(t0, W, K, wave_id(), rowof);
 }
 
-// Walk the wave's groups g = wave, wave + 4, ...; t0 holds group `wave` (gemv_prime). emit(g, rows,
-// acc) sees the R results on every lane (row < 0: no row).
+// Walk the wave's groups g = wave, wave + WS, ... (WS: the waves that walk, 0 .. WS - 1); t0 holds
+// group `wave` (gemv_prime). emit(g, rows, acc) sees the R results on every lane (row < 0: no row).
 #ifndef FX_PIPE_DEPTH
 #define FX_PIPE_DEPTH 2
 #endif
-template <class TileT, class WT, class RowFn, class XsFn, class EmitFn>
+template <int WS = FX_WAVES, class TileT, class WT, class RowFn, class XsFn, class EmitFn>
 __device__ __forceinline__ void gemv_pipe_x(TileT& t0, const WT& W, int K, XsFn xsof, int ngroups, RowFn& rowof,
                                             EmitFn emit) {
   TileT t1;
   float acc[TileT::kRows];
   int g = wave_id();
 #if FX_PIPE_DEPTH == 3
+  static_assert(WS == FX_WAVES, "the 3-deep walk uses every wave");
   // three tiles in rotation: while one is reduced, the next two are in flight
   TileT t2;
   if (g + FX_WAVES < ngroups) tile_load(t1, W, K, g + FX_WAVES, rowof);
@@ -195,12 +196,12 @@ __device__ __forceinline__ void gemv_pipe_x(TileT& t0, const WT& W, int K, XsFn 
   }
 #else
   while (g < ngroups) {
-    const int g1 = g + FX_WAVES;
+    const int g1 = g + WS;
     if (g1 < ngroups) tile_load(t1, W, K, g1, rowof);
     tile_dot(t0, xsof(g), K, acc);
     emit(g, t0.row, acc);
     if (g1 >= ngroups) break;
-    const int g2 = g1 + FX_WAVES;
+    const int g2 = g1 + WS;
     if (g2 < ngroups) tile_load(t0, W, K, g2, rowof);
     tile_dot(t1, xsof(g1), K, acc);
     emit(g1, t1.row, acc);
@@ -209,10 +210,10 @@ __device__ __forceinline__ void gemv_pipe_x(TileT& t0, const WT& W, int K, XsFn 
 #endif
 }
 // the same walk with one input row for every group
-template <class TileT, class WT, class RowFn, class EmitFn>
+template <int WS = FX_WAVES, class TileT, class WT, class RowFn, class EmitFn>
 __device__ __forceinline__ void gemv_pipe(TileT& t0, const WT& W, int K, const float* xs, int ngroups, RowFn& rowof,
                                           EmitFn emit) {
-  gemv_pipe_x(t0, W, K, [=](int) { return xs; }, ngroups, rowof, emit);
+  gemv_pipe_x<WS>(t0, W, K, [=](int) { return xs; }, ngroups, rowof, emit);
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -311,6 +312,55 @@ __device__ __forceinline__ void rmsnorm_staged(float* xs, const NormW& n, const 
   else rmsnorm_inplace(xs, wn, K, eps, red);
 }
 
+// The input row and its RMSNorm on ONE wave: a stage's control wave, which has no weight loads in
+// flight, so its polls return as soon as the packets exist (a wave's loads complete in issue order:
+// a poll behind a weight tile waits for the tile). Same arithmetic as rmsnorm_body: var =
+// sumsq_wave / K, rs = 1 / sqrt(var + eps), y = bf16(w * bf16(x * rs)). K <= 2048, a multiple of 8;
+// the caller syncs before other waves read xs.
+struct NormWave {
+  u32x4 w[4];   // chunks lane, lane + 64, lane + 128, lane + 192 of the norm weights
+};
+__device__ __forceinline__ NormWave norm_prefetch_wave(const uint16_t* wn, int K) {
+  NormWave n;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int c = lane_id() + 64 * j;
+    n.w[j] = c * 8 < K ? ld16(wn + c * 8) : u32x4{0u, 0u, 0u, 0u};
+  }
+  fx_issue_here();
+  return n;
+}
+__device__ __forceinline__ void poll_norm_wave(float* xs, const void* src, int K, float eps, const NormWave& n,
+                                               uint32_t tag, uint32_t* err) {
+  u32x4 v[8];
+  const int npairs = K >> 2;
+  pk_wait_pairs<8>(src, lane_id(), 64, npairs, tag, err, v);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int q = lane_id() + 64 * j;
+    if (q < npairs) {
+      xs[4 * q + 0] = bf_lo(v[j].x);
+      xs[4 * q + 1] = bf_hi(v[j].x);
+      xs[4 * q + 2] = bf_lo(v[j].z);
+      xs[4 * q + 3] = bf_hi(v[j].z);
+    }
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  const float ss = sumsq_wave(xs, K);
+  const float rs = 1.0f / sqrtf(ss / (float)K + eps);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int i = (lane_id() + 64 * j) * 8;
+    if (i < K) {
+      float w8[8];
+      unpack8(n.w[j], w8);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) xs[i + e] = bf16r(w8[e] * bf16r(xs[i + e] * rs));
+    }
+  }
+}
+
 // greedy id from the per-worker (max, index) packet pairs: the lowest index among the maxima (one
 // wave; result on every lane)
 __device__ __forceinline__ int64_t argmax_reduce(const void* amax, int nworkers, uint32_t tag, uint32_t* err) {
@@ -377,6 +427,10 @@ __device__ __forceinline__ void op_gemv_w(const fx_stage& s, FxEnv& env, const W
     // the workers of XCDs 0..6 (rank r of XCD x is worker r * 7 + x of 224)
     if (env.xcd == FX_XCDS - 1) return;
     range_split((s.n_rows + 3) >> 2, env.nworkers - FX_XWORKERS, env.xrank * (FX_XCDS - 1) + env.xcd, g0, g1);
+  } else if (s.flags & FX_F_LOW16) {
+    // ranks 0..15 of every XCD: workers 0..127 (worker = rank * 8 + XCD)
+    if (env.xrank >= FX_XWORKERS / 2) return;
+    range_split((s.n_rows + 3) >> 2, env.nworkers / 2, env.worker, g0, g1);
   } else {
     range_split((s.n_rows + 3) >> 2, env.nworkers, env.worker, g0, g1);
   }

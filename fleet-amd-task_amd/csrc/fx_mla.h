@@ -571,7 +571,7 @@ __device__ __forceinline__ void op_mla_attend(const fx_stage& s, FxEnv& env) {
 // (LDS, live floats) and red[0] are scratch. The caller syncs before reading xs.
 #define MERGE_BATCH 40   // splits whose partials are requested at once (every live split up to ctx 1280)
 __device__ __forceinline__ void merge_head(const void* part, int nh, int h, int prow, int d_c, int live, float* xs,
-                                           float* wj, float* red) {
+                                           float* wj, float* red, const FxEnv& env) {
   // wave 0 requests the lse of splits lane, lane + 64 first: loads complete in issue order, so the
   // weights below need not wait for the wave's partial-o loads
   float l0 = -__builtin_inff(), l1 = -__builtin_inff();
@@ -606,6 +606,7 @@ __device__ __forceinline__ void merge_head(const void* part, int nh, int h, int 
       for (int u = 0; u < n; ++u) den = den + __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), u));
     }
     if (lane_id() == 0) red[0] = den;
+    prof_mark(env, 4);
   }
   __syncthreads();
   // num = sum_j w_j o_j[c] in j order (fma)
@@ -624,6 +625,7 @@ __device__ __forceinline__ void merge_head(const void* part, int nh, int h, int 
       num[1] = __builtin_fmaf(w, __uint_as_float(o[k].y), num[1]);
     }
   }
+  prof_mark(env, 6);
   __syncthreads();
   const float den = red[0];
   xs[pc] = bf16r(num[0] / den);
@@ -669,7 +671,7 @@ __device__ __forceinline__ void op_mla_merge_uv(const fx_stage& s, FxEnv& env) {
   }
   __syncthreads();
   prof_mark(env, 1);
-  merge_head((const void*)s.x, nh, h, prow, d_c, live, xs, (float*)(env.lds + LDS_TILE), red);
+  merge_head((const void*)s.x, nh, h, prow, d_c, live, xs, (float*)(env.lds + LDS_TILE), red, env);
   const int pc = fx_tid() * 2;
   if (v0 == 0 && s.aux[4]) stc4((void*)s.aux[4], (uint32_t)(h * d_c + pc) * 2, pack2(xs[pc], xs[pc + 1]));
   __syncthreads();

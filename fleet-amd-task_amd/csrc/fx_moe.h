@@ -83,46 +83,78 @@ __device__ __forceinline__ void op_moe_router(const fx_stage& s, FxEnv& env) {
 // stream while the router logits are still on their way. With FX_F_ROUTER the stage also computes the router (row e on worker e, W_gate in `res`) and
 // reads the logits back from its own packets. act8[slot][i] = bf16(silu(bf16(W13[e][i] h)) *
 // bf16(W13[e][I + i] h)).
+// w13_prime issues the loads that need nothing from the stage's inputs (each wave's first shared
+// group, the router row, the norm weights); w13_main does the rest. The stage runs them back to
+// back; a GEMV stage flagged FX_F_PAIR runs w13_prime of the next stage before its own work (run_pair).
+template <class TileT>
+struct W13Pre {
+  TileT t0;          // the wave's first shared group
+  Tile<1, 4> tr;     // the router row (worker e < E, wave 0)
+  NormW nw;
+};
+// the worker's shared groups [a0, a1) and routed groups [b0, b1) (pair groups of 4 rows: p, I + p,
+// p + 1, I + p + 1; PG = I / 2 per slot). The shared slots' nsh * PG groups and the routed slots'
+// topk * PG groups are each split evenly over the workers, so every worker streams the same number
+// of rows (within one group)
+struct W13Split {
+  int a0, a1, b0, b1;
+};
+__device__ __forceinline__ W13Split w13_split(const fx_stage& s, const FxEnv& env) {
+  W13Split q;
+  const int PG = s.n_rows >> 1;
+  range_split(s.n_forced * PG, env.nworkers, env.worker, q.a0, q.a1);
+  range_split(s.topk * PG, env.nworkers, env.worker, q.b0, q.b1);
+  return q;
+}
 template <class TileT, class WT>
-__device__ __forceinline__ void op_moe_w13_t(const fx_stage& s, FxEnv& env, const WT& W) {
+__device__ __forceinline__ void w13_prime(const fx_stage& s, const FxEnv& env, const WT& W, W13Pre<TileT>& p) {
+  const int K = s.k, I = s.n_rows, E = s.aux_i0, PG = I >> 1;
+  const W13Split q = w13_split(s, env);
+  const size_t ex = (size_t)2 * I;
+  auto rowA = [&](int g, int i) {
+    const int a = q.a0 + g;
+    const int e = E + a / PG;
+    const int pp = 2 * (a % PG) + (i >> 1);
+    return (int)(e * ex + ((i & 1) ? I + pp : pp));
+  };
+  gemv_prime(p.t0, W, K, q.a1 - q.a0, rowA);
+  const bool rrow = (s.flags & FX_F_ROUTER) && env.worker < E;
+  auto rowR = [&](int g, int i) { return env.worker; };
+  if (rrow && wave_id() == 0) tile_load(p.tr, (const uint16_t*)s.res, K, 0, rowR);
+  p.nw = K <= 8 * FX_THREADS ? norm_prefetch((const uint16_t*)s.w_norm, K) : NormW{};
+}
+template <class TileT, class WT>
+__device__ __forceinline__ void w13_main(const fx_stage& s, FxEnv& env, const WT& W, W13Pre<TileT>& p) {
   float* xs = (float*)(env.lds + LDS_XS);
   float* red = (float*)(env.lds + LDS_RED);
   int* ids = (int*)(env.lds + LDS_MISC + 128);
   float* wts = (float*)(env.lds + LDS_MISC + 256);
   const int K = s.k, I = s.n_rows, E = s.aux_i0;
-  const int topk = s.topk, nsh = s.n_forced;
+  const int topk = s.topk;
   const bool router = (s.flags & FX_F_ROUTER) != 0;
   const bool writer = env.worker == 0;
   float* lg = red + 256;
-  // pair groups (2 pairs = rows p, I + p, p + 1, I + p + 1) of a slot: PG = I / 2. The shared
-  // slots' nsh * PG groups and the routed slots' topk * PG groups are each split evenly over the
-  // workers, so every worker streams the same number of rows (within one group)
   const int PG = I >> 1;
-  int a0, a1, b0, b1;
-  range_split(nsh * PG, env.nworkers, env.worker, a0, a1);
-  range_split(topk * PG, env.nworkers, env.worker, b0, b1);
-  const int nA = a1 - a0, nB = b1 - b0;
+  const W13Split q = w13_split(s, env);
+  const int a0 = q.a0, b0 = q.b0;
+  const int nA = q.a1 - q.a0, nB = q.b1 - q.b0;
   const size_t ex = (size_t)2 * I;   // rows per expert
   auto rowA = [&](int g, int i) {
     const int a = a0 + g;
     const int e = E + a / PG;
-    const int p = 2 * (a % PG) + (i >> 1);
-    return (int)(e * ex + ((i & 1) ? I + p : p));
+    const int pp = 2 * (a % PG) + (i >> 1);
+    return (int)(e * ex + ((i & 1) ? I + pp : pp));
   };
   auto rowB = [&](int g, int i) {
     const int r = b0 + g;
     const int e = ids[r / PG];
-    const int p = 2 * (r % PG) + (i >> 1);
-    return (int)(e * ex + ((i & 1) ? I + p : p));
+    const int pp = 2 * (r % PG) + (i >> 1);
+    return (int)(e * ex + ((i & 1) ? I + pp : pp));
   };
-  TileT t0;
-  gemv_prime(t0, W, K, nA, rowA);
+  TileT& t0 = p.t0;
   const bool rrow = router && env.worker < E;
-  const uint16_t* Wg = (const uint16_t*)s.res;
-  auto rowR = [&](int g, int i) { return env.worker; };
-  Tile<1, 4> tr;
-  if (rrow && wave_id() == 0) tile_load(tr, Wg, K, 0, rowR);
-  const NormW nw = K <= 8 * FX_THREADS ? norm_prefetch((const uint16_t*)s.w_norm, K) : NormW{};
+  Tile<1, 4>& tr = p.tr;
+  const NormW& nw = p.nw;
   poll_row(xs, (const void*)s.x, K, tag_in(s, env, 1), env.err);
   prof_mark(env, 1);
   rmsnorm_staged(xs, nw, (const uint16_t*)s.w_norm, K, s.eps, red);
@@ -157,7 +189,9 @@ __device__ __forceinline__ void op_moe_w13_t(const fx_stage& s, FxEnv& env, cons
   // routed slots: the top-k of the logits, on the last wave (groups g = wave, wave + 4, ..: it has
   // the fewest shared groups, so it polls the logits while the others finish theirs)
   if (wave_id() == FX_WAVES - 1) {
+    prof_mark_wave(env, 7);
     poll_logits_wave(lg, (const void*)s.aux[0], E, router ? tag : tag_in(s, env, 0), env.err);
+    prof_mark_wave(env, 6);
     float* probs = red + 512;
     route_slots_wave(lg, s, ids, wts, probs);
     if (writer) {
@@ -196,7 +230,6 @@ __device__ __forceinline__ void op_moe_w13_t(const fx_stage& s, FxEnv& env, cons
   }
   // the routing stays in LDS for the expert-down stage that follows on this worker
   env.route_tag = router ? tag : tag_in(s, env, 0);
-  prof_mark(env, 6);
   // The routed groups are walked by whole waves up to a multiple of the wave count; one group left
   // over (the split gives every other worker 17 at V2-Lite's shapes) is split by rows, row w on wave
   // w, its loads requested ahead of the walk: the worker then ends a quarter tile after its
@@ -238,9 +271,14 @@ __device__ __forceinline__ void op_moe_w13(const fx_stage& s, FxEnv& env) {
   if constexpr (kFp8) {
     const size_t rows = (size_t)(s.aux_i0 + s.n_forced) * 2 * s.n_rows;
     const Fp8W W{(const uint8_t*)s.w, (const float*)((const uint8_t*)s.w + rows * (size_t)s.k)};
-    op_moe_w13_t<TileQ<4, 2>>(s, env, W);
+    W13Pre<TileQ<4, 2>> p;
+    w13_prime(s, env, W, p);
+    w13_main(s, env, W, p);
   } else {
-    op_moe_w13_t<Tile<4, 4>>(s, env, (const uint16_t*)s.w);
+    const uint16_t* W = (const uint16_t*)s.w;
+    W13Pre<Tile<4, 4>> p;
+    w13_prime(s, env, W, p);
+    w13_main(s, env, W, p);
   }
 }
 

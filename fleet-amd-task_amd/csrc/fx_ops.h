@@ -39,3 +39,32 @@ __device__ __forceinline__ void run_stage(const fx_stage& s, FxEnv& env) {
     default: break;
   }
 }
+
+// A GEMV stage flagged FX_F_PAIR and the MOE_W13 stage after it as one operator: the expert
+// stage's first weight loads (w13_prime: its shared groups, the router row, the norm weights) are
+// issued before the GEMV's own, so they stream while the GEMV waits for its input (o_proj waits for
+// the attention chain, with the HBM otherwise idle) and the expert stage starts with them in
+// registers and no weight loads queued ahead of its polls. `pst_next`: the second stage's profile
+// stamps; env.sidx / env.pst are switched to the second stage for its part.
+template <bool kFp8, class TileT, class WT>
+__device__ __forceinline__ void run_pair_w(const fx_stage& g, const fx_stage& m, FxEnv& env, uint64_t* pst_next,
+                                           const WT& W) {
+  W13Pre<TileT> p;
+  w13_prime(m, env, W, p);
+  run_stage<kFp8>(g, env);
+  prof_mark(env, 3);
+  env.sidx = env.sidx + 1;
+  env.pst = pst_next;
+  prof_mark(env, 0);
+  w13_main(m, env, W, p);
+}
+template <bool kFp8>
+__device__ __forceinline__ void run_pair(const fx_stage& g, const fx_stage& m, FxEnv& env, uint64_t* pst_next) {
+  if constexpr (kFp8) {
+    const size_t rows = (size_t)(m.aux_i0 + m.n_forced) * 2 * m.n_rows;
+    const Fp8W W{(const uint8_t*)m.w, (const float*)((const uint8_t*)m.w + rows * (size_t)m.k)};
+    run_pair_w<kFp8, TileQ<4, 2>>(g, m, env, pst_next, W);
+  } else {
+    run_pair_w<kFp8, Tile<4, 4>>(g, m, env, pst_next, (const uint16_t*)m.w);
+  }
+}

@@ -7,6 +7,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <vector>
+
 #include "fx_device.h"
 
 #define PROBE_LIMIT (100ull * 1000 * 1000)   // 1 s of s_memrealtime ticks: every wait gives up after it
@@ -266,6 +268,153 @@ __global__ void fxp_pingpong_kernel(uint32_t* flag, int a, int b, uint32_t round
       break;
   }
   if (acc == 0x12345678u) out[2] = acc;
+}
+
+// ---- loaded round trip: blocks a and b ping-pong a flag with sc1 stores and loads (the decode
+// kernel's packet policy) for `rounds` round trips while every other block streams its share of
+// `load` without a pause: a wave keeps between D and 2D 1 KiB non-temporal loads in flight
+// (double-buffered tiles, wrapping over the block's share), so D sets the depth of the memory
+// queues the flag's stores and loads meet. Per streaming block: bytes read and ticks until it saw
+// the stop flag (bounded by PROBE_LIMIT like every wait here).
+template <int D>
+__device__ void loaded_stream(const uint8_t* base, uint64_t per, const uint32_t* stop, uint64_t* bytes_out,
+                              uint64_t* ticks_out, int work) {
+  __shared__ uint64_t wave_bytes[16];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  const uint64_t step = (uint64_t)nw * D * 1024;
+  const uint64_t span = per - per % step;
+  uint32_t acc = 0;
+  uint64_t off = (uint64_t)wave * D * 1024, nbytes = 0;
+  auto load = [&](u32x4p* v, uint64_t o0) {
+#pragma unroll
+    for (int d = 0; d < D; ++d)
+      v[d] = __builtin_nontemporal_load((const u32x4p*)(base + o0 + (uint64_t)d * 1024 + lane * 16));
+  };
+  // `work` dependent fmas per KiB loaded: the VALU time a GEMV tile spends per KiB
+  float f = (float)lane;
+  auto use = [&](const u32x4p* v) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      acc += v[d].x ^ v[d].y ^ v[d].z ^ v[d].w;
+      for (int k = 0; k < work; ++k) f = __builtin_fmaf(f, 0.999f, __uint_as_float(v[d].x & 0x3f800000u));
+    }
+  };
+  auto next = [&](uint64_t o) { o += step; return o >= span ? o - span : o; };
+  u32x4p a[D], b[D];
+  const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+  load(a, off);
+  for (uint32_t it = 0;; ++it) {
+    off = next(off);
+    load(b, off);
+    use(a);
+    off = next(off);
+    load(a, off);
+    use(b);
+    nbytes += 2 * D * 1024;
+    if ((it & 7) == 7 && (__hip_atomic_load(stop, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ||
+                          __builtin_amdgcn_s_memrealtime() - t0 > PROBE_LIMIT))
+      break;
+  }
+  use(a);
+  if (lane == 0) wave_bytes[wave] = nbytes;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint64_t tot = 0;
+    for (int w = 0; w < nw; ++w) tot += wave_bytes[w];
+    bytes_out[blockIdx.x] = tot;
+    ticks_out[blockIdx.x] = __builtin_amdgcn_s_memrealtime() - t0;
+  }
+  if (acc == 0x12345678u || f == 1234.5f) bytes_out[gridDim.x] = acc;
+}
+
+// waves 1 .. of a ping-pong block stream their block's share the same way (self < 0: they exit),
+// so the flag's loads share the CU with a stream; no block-wide barrier (wave 0 is elsewhere)
+template <int D>
+__device__ void self_stream(const uint8_t* base, uint64_t per, const uint32_t* stop) {
+  const int lane = threadIdx.x & 63, wave = (threadIdx.x >> 6) - 1, nw = (blockDim.x >> 6) - 1;
+  const uint64_t step = (uint64_t)nw * D * 1024;
+  const uint64_t span = per - per % step;
+  uint32_t acc = 0;
+  uint64_t off = (uint64_t)wave * D * 1024;
+  auto load = [&](u32x4p* v, uint64_t o0) {
+#pragma unroll
+    for (int d = 0; d < D; ++d)
+      v[d] = __builtin_nontemporal_load((const u32x4p*)(base + o0 + (uint64_t)d * 1024 + lane * 16));
+  };
+  auto use = [&](const u32x4p* v) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) acc += v[d].x ^ v[d].y ^ v[d].z ^ v[d].w;
+  };
+  auto next = [&](uint64_t o) { o += step; return o >= span ? o - span : o; };
+  u32x4p a[D], b[D];
+  const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+  load(a, off);
+  for (uint32_t it = 0;; ++it) {
+    off = next(off);
+    load(b, off);
+    use(a);
+    off = next(off);
+    load(a, off);
+    use(b);
+    if ((it & 7) == 7 && (__hip_atomic_load(stop, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ||
+                          __builtin_amdgcn_s_memrealtime() - t0 > PROBE_LIMIT))
+      break;
+  }
+  use(a);
+  if (acc == 0x12345678u) *(uint32_t*)(base) = acc;
+}
+
+__global__ void __launch_bounds__(256) fxp_loaded_kernel(uint32_t* flag, int a, int b, uint32_t rounds, int depth,
+                                                         int work, const uint8_t* load, uint64_t load_bytes,
+                                                         uint64_t* bytes_out, uint64_t* ticks_out, uint64_t* out) {
+  const int blk = blockIdx.x;
+  if (blk == a || blk == b) {
+    // work < 0: waves 1 .. of the ping-pong blocks stream too (depth -work)
+    if (threadIdx.x >= 64) {
+      if (work < 0 && load) {
+        const uint64_t per = load_bytes / gridDim.x;
+        const uint8_t* base = load + (uint64_t)blk * per;
+        if (work == -4) self_stream<4>(base, per, &flag[64]);
+        else if (work == -8) self_stream<8>(base, per, &flag[64]);
+        else self_stream<16>(base, per, &flag[64]);
+      }
+      return;
+    }
+    if (threadIdx.x == 0) {
+      // a short idle delay so the streams are running before the first round trip
+      const uint64_t ts = __builtin_amdgcn_s_memrealtime();
+      while (__builtin_amdgcn_s_memrealtime() - ts < 2000) __builtin_amdgcn_s_sleep(8);
+      const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+      bool ok = true;
+      for (uint32_t i = 1; i <= rounds && ok; ++i) {
+        if (blk == a) {
+          pp_st(&flag[0], i, 2);
+          while (pp_ld(&flag[32], 2) != i)
+            if (__builtin_amdgcn_s_memrealtime() - t0 > PROBE_LIMIT) { ok = false; break; }
+        } else {
+          while (pp_ld(&flag[0], 2) != i)
+            if (__builtin_amdgcn_s_memrealtime() - t0 > PROBE_LIMIT) { ok = false; break; }
+          pp_st(&flag[32], i, 2);
+        }
+      }
+      if (blk == a) {
+        out[0] = __builtin_amdgcn_s_memrealtime() - t0;
+        out[1] = ok ? 1 : 0;
+        __hip_atomic_store(&flag[64], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+    return;
+  }
+  if (!load || depth == 0) return;
+  const uint64_t per = load_bytes / gridDim.x;
+  const uint8_t* base = load + (uint64_t)blk * per;
+  if (work < 0) work = 0;
+  if (depth == 1) loaded_stream<1>(base, per, &flag[64], bytes_out, ticks_out, work);
+  else if (depth == 2) loaded_stream<2>(base, per, &flag[64], bytes_out, ticks_out, work);
+  else if (depth == 4) loaded_stream<4>(base, per, &flag[64], bytes_out, ticks_out, work);
+  else if (depth == 8) loaded_stream<8>(base, per, &flag[64], bytes_out, ticks_out, work);
+  else if (depth == 16) loaded_stream<16>(base, per, &flag[64], bytes_out, ticks_out, work);
+  else loaded_stream<24>(base, per, &flag[64], bytes_out, ticks_out, work);
 }
 
 // ---- lane exchange check: out[lane * 6 + k] = the value xor_lane<2^k> returns on `lane` when every
@@ -538,6 +687,48 @@ int fxp_pingpong(int a, int b, uint32_t rounds, int mode, const void* load, uint
   (void)hipFree(flag);
   (void)hipFree(out);
   return e;
+}
+
+// out_host[0] = round-trip ticks for `rounds`, [1] = 1 if every round completed, [2] = bytes the
+// streaming blocks read, [3] = their mean ticks until they stopped
+int fxp_loaded(int a, int b, uint32_t rounds, int depth, int work, const void* load, uint64_t load_bytes, int blocks,
+               int threads, uint64_t* out_host) {
+  if (depth != 0 && depth != 1 && depth != 2 && depth != 4 && depth != 8 && depth != 16 && depth != 24) return -1;
+  if (a < 0 || b < 0 || a >= blocks || b >= blocks || a == b || threads % 64 || threads > 256 || threads < 128) return -1;
+  if (work < 0 && work != -4 && work != -8 && work != -16) return -1;
+  uint32_t* flag = nullptr;
+  uint64_t *out = nullptr, *bo = nullptr, *to = nullptr;
+  hipError_t e;
+  if ((e = hipMalloc(&flag, 1024)) != hipSuccess) return e;
+  if ((e = hipMalloc(&out, 64)) != hipSuccess) return e;
+  if ((e = hipMalloc(&bo, (blocks + 1) * 8)) != hipSuccess) return e;
+  if ((e = hipMalloc(&to, blocks * 8)) != hipSuccess) return e;
+  (void)hipMemset(flag, 0, 1024);
+  (void)hipMemset(out, 0, 64);
+  (void)hipMemset(bo, 0, (blocks + 1) * 8);
+  (void)hipMemset(to, 0, blocks * 8);
+  void* args[] = {&flag, &a, &b, &rounds, &depth, &work, (void*)&load, &load_bytes, &bo, &to, &out};
+  if ((e = hipLaunchCooperativeKernel((const void*)fxp_loaded_kernel, dim3(blocks), dim3(threads), args, 0, 0)) !=
+      hipSuccess)
+    return e;
+  if ((e = hipDeviceSynchronize()) != hipSuccess) return e;
+  uint64_t o[2];
+  std::vector<uint64_t> hb(blocks), ht(blocks);
+  if ((e = hipMemcpy(o, out, 16, hipMemcpyDeviceToHost)) != hipSuccess) return e;
+  if ((e = hipMemcpy(hb.data(), bo, blocks * 8, hipMemcpyDeviceToHost)) != hipSuccess) return e;
+  if ((e = hipMemcpy(ht.data(), to, blocks * 8, hipMemcpyDeviceToHost)) != hipSuccess) return e;
+  uint64_t tb = 0, tt = 0, n = 0;
+  for (int i = 0; i < blocks; ++i)
+    if (i != a && i != b && ht[i]) { tb += hb[i]; tt += ht[i]; ++n; }
+  out_host[0] = o[0];
+  out_host[1] = o[1];
+  out_host[2] = tb;
+  out_host[3] = n ? tt / n : 0;
+  (void)hipFree(flag);
+  (void)hipFree(out);
+  (void)hipFree(bo);
+  (void)hipFree(to);
+  return 0;
 }
 
 int fxp_dot2(const uint32_t* a_host, const uint32_t* b_host, const float* c_host, float* d_host, int n) {

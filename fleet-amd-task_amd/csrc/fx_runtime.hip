@@ -88,7 +88,15 @@ __device__ __forceinline__ void persistent_body(const FxRunArgs& a) {
       env.sidx = s;
       env.pst = prof ? a.prof + ((size_t)s * FX_BLOCKS + b) * FX_PROF_SLOTS : nullptr;
       prof_mark(env, 0);
-      run_stage<kFp8>(*sst, env);
+      if (sst->flags & FX_F_PAIR) {
+        // this GEMV and the expert gate|up stage after it as one operator (fx_load_plan checked the
+        // pair): the second stage's profile stamps and index are its own
+        run_pair<kFp8>(*sst, table[s + 1], env,
+                       prof ? a.prof + ((size_t)(s + 1) * FX_BLOCKS + b) * FX_PROF_SLOTS : nullptr);
+        ++s;
+      } else {
+        run_stage<kFp8>(*sst, env);
+      }
       if (prof) {
         __syncthreads();
         prof_mark(env, 3);
@@ -406,6 +414,8 @@ static int check_stage(fx_ctx* c, const fx_stage& s, int idx, int n_total) {
   if ((s.flags & FX_F_XCD) && (s.flags & FX_F_MFMA)) return bad("FX_F_XCD and FX_F_MFMA exclude each other");
   if ((s.flags & FX_F_SKIP_XCD) && (s.op != FX_OP_GEMV || (s.flags & FX_F_ARGMAX)))
     return bad("FX_F_SKIP_XCD marks a GEMV without argmax only");
+  if ((s.flags & FX_F_LOW16) && (s.op != FX_OP_GEMV || (s.flags & (FX_F_ARGMAX | FX_F_SKIP_XCD))))
+    return bad("FX_F_LOW16 marks a GEMV without argmax or FX_F_SKIP_XCD only");
   if (s.flags & FX_F_FP8) {
     const bool head = s.op == FX_OP_GEMV && (s.flags & FX_F_ARGMAX) && s.in_kind == FX_IN_VEC;
     if (s.op != FX_OP_MOE_W13 && s.op != FX_OP_MOE_W2 && !head)
@@ -424,7 +434,8 @@ static int check_stage(fx_ctx* c, const fx_stage& s, int idx, int n_total) {
       if ((s.flags & FX_F_RESIDUAL) && !s.res) return bad("residual");
       if ((s.flags & FX_F_RES_EMBED) && !s.aux[0]) return bad("embedding residual");
       const int groups = (s.n_rows + 3) / 4;
-      const int rows_max = 4 * ((groups + FX_WORKERS - 1) / FX_WORKERS);
+      const int gworkers = (s.flags & FX_F_LOW16) ? FX_WORKERS / 2 : FX_WORKERS;
+      const int rows_max = 4 * ((groups + gworkers - 1) / gworkers);
       if ((s.flags & (FX_F_OUT_LL | FX_F_RESIDUAL | FX_F_RES_EMBED)) && rows_max > FX_MAX_OUT_ROWS / 2)
         return bad("rows per worker exceed the LDS row table");
       if ((s.flags & FX_F_OUT_LL) && s.n_rows % 4) return bad("packet output needs rows in multiples of 4");
@@ -496,6 +507,17 @@ int fx_load_plan(fx_ctx* c, const fx_stage* st, int32_t n, const fx_stage* epi, 
   for (int i = 0; i < n_epi; ++i) {
     int r = check_stage(c, epi[i], n + i, n);
     if (r) return r;
+  }
+  // FX_F_PAIR: a GEMV that the persistent kernel runs together with the MOE_W13 stage after it
+  for (int i = 0; i < n + n_epi; ++i) {
+    const fx_stage& t = i < n ? st[i] : epi[i - n];
+    if (!(t.flags & FX_F_PAIR)) continue;
+    const std::string at = "stage " + std::to_string(i) + ": FX_F_PAIR ";
+    if (i >= n - 1) return fail(c, FX_E_ARG, at + "needs a MOE_W13 stage after it in the plan");
+    if (t.op != FX_OP_GEMV || (t.flags & (FX_F_ARGMAX | FX_F_HEAD | FX_F_SKIP_XCD | FX_F_FP8)))
+      return fail(c, FX_E_ARG, at + "is for a plain GEMV stage");
+    if (st[i + 1].op != FX_OP_MOE_W13 || (st[i + 1].flags & (FX_F_HEAD | FX_F_PAIR)))
+      return fail(c, FX_E_ARG, at + "needs a MOE_W13 stage after it");
   }
   // a plan's expert stages are all bf16 or all FP8: the launch picks the kernel variant
   int n_fp8 = 0, n_exp = 0;

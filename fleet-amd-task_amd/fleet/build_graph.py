@@ -236,6 +236,17 @@ def compile_stages(plan, host):
             else:
                 assert name == "amax", f"{labels[i]}: no stage writes {name}"
                 stages[i].src[k] = -1
+    if getattr(plan, "pair", False):
+        # o_proj + the MoE gate|up stage after it: one operator of the persistent kernel (FX_F_PAIR)
+        no = R.FX_F_ARGMAX | R.FX_F_HEAD | R.FX_F_SKIP_XCD | R.FX_F_FP8
+        for i in range(n - 1):
+            if (stages[i].op == R.FX_OP_GEMV and not (stages[i].flags & no)
+                    and stages[i + 1].op == R.FX_OP_MOE_W13 and not (stages[i + 1].flags & R.FX_F_HEAD)):
+                stages[i].flags |= R.FX_F_PAIR
+                if plan.attn == "mfma" and i > 0 and stages[i - 1].op == R.FX_OP_MLA_MERGE_UV:
+                    # the merge's workers (ranks 16..31) take no o_proj rows: they go straight on to
+                    # the expert stage's first loads
+                    stages[i].flags |= R.FX_F_LOW16
     epi_st = []
     for st, ins in epi:
         for k, name in ins:

@@ -87,6 +87,7 @@ class Plan:
     fp8_experts: bool = False   # W13 / W2 are FP8 (codes + per-row scales, pack_weights.quantize_experts)
     fp8_head: bool = False      # W_lm is FP8 too (pack_weights.quantize_head; needs fp8_experts)
     attn: str = "mfma"          # attention kernel: "mfma" (matrix cores, splits over all workers) or "valu"
+    pair: bool = True           # o_proj and the expert gate|up stage after it run as one operator (FX_F_PAIR)
 
     def t(self, name, shape, dtype="bf16", kind="new", source=""):
         assert name not in self.tensors, name
@@ -172,11 +173,14 @@ def default_splits(s_max, attn="mfma"):
 
 def build_plan(dims: Dims = REAL_DIMS, s_max: int = 1056, layers: int = 27, head: bool = True, split: int = None,
                n_splits: int = None, iters_cap: int = 32, softmax_scale: float = SOFTMAX_SCALE,
-               eps: float = RMS_EPS, fp8_experts: bool = False, fp8_head: bool = False, attn: str = None) -> Plan:
+               eps: float = RMS_EPS, fp8_experts: bool = False, fp8_head: bool = False, attn: str = None,
+               pair: bool = True) -> Plan:
     """split / n_splits: the attention split (positions) or split count; neither: default_splits.
     attn: "mfma" (the matrix-core attention: splits over all workers, every head per split), "xcd"
     (the same attention and its merge on the 32 workers of one XCD, partials in its L2), "valu"
-    (heads over XCDs, score chains on the vector ALUs), or None: default_attn(s_max)."""
+    (heads over XCDs, score chains on the vector ALUs), or None: default_attn(s_max).
+    pair: each MoE layer's o_proj issues the expert gate|up stage's first weight loads while it waits
+    for the attention (the two run as one operator of the persistent kernel; same results)."""
     d = dims
     assert 1 <= layers <= d.L
     attn = default_attn(s_max) if attn is None else attn
@@ -184,6 +188,7 @@ def build_plan(dims: Dims = REAL_DIMS, s_max: int = 1056, layers: int = 27, head
     split, n_splits = splits_for(s_max, split, n_splits) if (split or n_splits) else default_splits(s_max, attn)
     p = Plan(d, s_max, layers, head, split, n_splits)
     p.attn = attn
+    p.pair = pair
     p.scale = softmax_scale
     p.eps = eps
     p.fp8_experts = fp8_experts

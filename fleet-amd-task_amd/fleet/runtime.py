@@ -29,6 +29,8 @@ FX_F_MFMA = 512
 FX_F_XLOCAL = 1024
 FX_F_XCD = 2048
 FX_F_SKIP_XCD = 4096
+FX_F_PAIR = 8192
+FX_F_LOW16 = 16384
 FX_MAX_ITERS, FX_MAX_MARKS, FX_PROF_SLOTS = 65536, 256, 8
 FX_ABI_VERSION = 4
 WORKERS = 256          # one worker workgroup per CU

@@ -73,8 +73,9 @@ def report(rows, d, ctx, iter_us=None):
     if marked:
         lines += ["", "Operator-internal points (median over workers, µs after the worker's inputs arrived):",
                   "attention: 4 first tile scored, 5 softmaxed, 6 value product done, 7 partials complete; "
-                  "merge: 4 lse weights, 5 merged o; w13: 4 normed (+ router row), 5 shared slots done, 6 top-k "
-                  "known; w2: 4 shared slots done, 5 routed activations arrived; GEMV (qkva, o_proj, dense down, LM head): "
+                  "merge: 4 lse weights, 6 weighted sums, 5 merged o; w13: 4 normed (+ router row), 5 shared slots "
+                  "done (wave 0), 7 logits polled from, 6 logits arrived (the last wave); w2: 4 shared slots done, 5 routed "
+                  "activations arrived; GEMV (qkva, o_proj, dense down, LM head): "
                   "4 input normed, 5 rows done", "", "| stage | 4 | 5 | 6 | 7 |", "|---|---|---|---|---|"]
         for r in marked[:16]:
             cells = " | ".join("-" if m is None else f"{m:.2f}" for m in r["marks"])
@@ -95,6 +96,7 @@ def main():
     ap.add_argument("--json", default=None)
     ap.add_argument("--n-splits", type=int, default=None, help="attention split count (default: the plan's own)")
     ap.add_argument("--split", type=int, default=None, help="attention split length (a multiple of 32)")
+    ap.add_argument("--no-pair", action="store_true", help="o_proj and the expert gate|up as two operators")
     ap.add_argument("--attn", choices=("mfma", "xcd", "valu"), default=None,
                     help="attention kernel (default: the plan's own choice)")
     ap.add_argument("--fp8-experts", action="store_true", help="FP8 expert weights (pack_weights.quantize_experts)")
@@ -109,7 +111,8 @@ def main():
         global EXPERT_BYTES
         EXPERT_BYTES = 1
     prompt = P.prompt_ids(args.seed, ctx, d.V)
-    kw = dict(split=args.split, n_splits=args.n_splits, fp8_experts=args.fp8_experts, attn=args.attn)
+    kw = dict(split=args.split, n_splits=args.n_splits, fp8_experts=args.fp8_experts, attn=args.attn,
+              pair=not args.no_pair)
     plan = G.build_plan(d, s_max, args.layers, True, **kw)
     runner = B.build(rt, bufs, B.make_capture(rt, plan), B.make_meta(rt, s_max, prompt), d, s_max, args.layers, True,
                      **kw)

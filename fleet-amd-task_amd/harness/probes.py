@@ -32,6 +32,8 @@ def probe_lib():
     L.fxp_chase.argtypes = [vp, u32, ctypes.c_int, vp, u64, ctypes.c_int, ctypes.POINTER(u64)]
     L.fxp_pingpong.argtypes = [ctypes.c_int, ctypes.c_int, u32, ctypes.c_int, vp, u64, ctypes.c_int,
                                ctypes.POINTER(u64)]
+    L.fxp_loaded.argtypes = [ctypes.c_int, ctypes.c_int, u32, ctypes.c_int, ctypes.c_int, vp, u64, ctypes.c_int,
+                             ctypes.c_int, ctypes.POINTER(u64)]
     L.fxp_lanes.argtypes = [ctypes.POINTER(ctypes.c_float)]
     L.fxp_valu.argtypes = [ctypes.POINTER(u64)]
     L.fxp_icache.argtypes = [vp, u64, ctypes.POINTER(u64)]
@@ -59,6 +61,8 @@ def main():
     ap.add_argument("--clock", action="store_true")
     ap.add_argument("--pingpong-only", action="store_true", help="only the flag round trips")
     ap.add_argument("--valu", action="store_true", help="only the VALU issue rate of FMA chains")
+    ap.add_argument("--loaded", action="store_true",
+                    help="only the sc1 flag round trip against the depth of a concurrent full-chip stream")
     ap.add_argument("--reuse", action="store_true",
                     help="cold (first touch) against warm (re-read) streams, register and direct-to-LDS loads")
     args = ap.parse_args()
@@ -99,6 +103,26 @@ def main():
             print(f"instruction fetch ({'under stream' if load else 'idle'}, launch {rep}): 4096 x 8-byte v_fmac_f32 "
                   f"straight-line, cold pass {oc[0]} cycles ({oc[0] / 4096:.2f}/instr), warm pass {oc[1]} cycles "
                   f"({oc[1] / 4096:.2f}/instr)", flush=True)
+        rt.close()
+        return
+    if args.loaded:
+        big = rt.alloc((2 << 30,), "u8")
+        out = (ctypes.c_uint64 * 4)()
+        print("| a (XCD) | b (XCD) | stream KiB in flight per wave | fma per KiB (< 0: the flag blocks' own waves "
+              "stream too, -x KiB tiles) | ns/round trip | stream GB/s |", flush=True)
+        print("|---|---|---|---|---|---|", flush=True)
+        # fma per KiB < 0: the ping-pong blocks' other waves stream too, -fma KiB per tile
+        for a, b in ((8, 9), (8, 16)):
+            for work in (0, -4, -16, 16):
+                for depth in (0, 2, 4, 8, 16, 24):
+                    if depth == 0 and work > 0:
+                        continue
+                    rc = L.fxp_loaded(a, b, 2000, depth, work, ctypes.c_void_p(big.ptr), big.nbytes, 256, 256, out)
+                    assert rc == 0, rc
+                    rt_ns = f"{out[0] * TICK_NS / 2000:.0f}" if out[1] == 1 else "no round trip within 1 s"
+                    gbs = out[2] / (out[3] * TICK_NS) if out[3] else 0.0
+                    fl = "idle" if depth == 0 else f"{depth}..{2 * depth}"
+                    print(f"| {a} ({a % 8}) | {b} ({b % 8}) | {fl} | {work} | {rt_ns} | {gbs:.0f} |", flush=True)
         rt.close()
         return
     if args.clock:

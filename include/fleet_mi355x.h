@@ -132,6 +132,14 @@ enum fx_op {
                             * packets, scale, s_max; src[0] = their producer */
 #define FX_F_SKIP_XCD 4096u /* GEMV: rows split over the workers of XCDs 0..6 only (XCD 7 runs the
                             * single-XCD attention just before) */
+#define FX_F_LOW16 16384u  /* GEMV: rows split over ranks 0..15 of every XCD (workers 0..127) only: the
+                            * matrix-core attention's merge runs on ranks 16..31 just before, and those
+                            * workers go on to the expert stage's first loads instead (FX_F_PAIR) */
+#define FX_F_PAIR 8192u    /* GEMV followed by a MOE_W13 stage: the persistent kernel runs the two as one
+                            * operator that issues the expert stage's first weight loads (its shared
+                            * groups, router row, norm weights) before the GEMV's own, so they stream while
+                            * the GEMV waits for its input. The kernel suite's one-stage launches ignore
+                            * the flag. Not with FX_F_ARGMAX, FX_F_HEAD or FX_F_SKIP_XCD */
 
 /* One entry of the task table: one operator of the plan (fleet/graph_plan.py Call). */
 typedef struct fx_stage {
