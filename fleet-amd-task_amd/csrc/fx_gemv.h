@@ -216,6 +216,123 @@ __device__ __forceinline__ void gemv_pipe(TileT& t0, const WT& W, int K, const f
   gemv_pipe_x<WS>(t0, W, K, [=](int) { return xs; }, ngroups, rowof, emit);
 }
 
+// The same walk at the granularity of one chunk column: a slice is the R rows' chunk j (R KiB), and
+// the wave keeps D slices in flight instead of two whole tiles, so a CU queues D x R x 4 KiB of weight
+// loads rather than 2 x R x NJ x 4 KiB: its later polls wait behind less. The arithmetic is
+// tile_dot's (each row's chunks in increasing j, then the butterfly). rowof(g, i) as for the tiles.
+// The first D slices of group `wave` are issued by slices_prime.
+template <int R, int D>
+struct SliceRing {
+  u32x4 w[D][R];
+  int row[R];
+};
+template <int R, class RowFn>
+__device__ __forceinline__ void slice_rows(int (&row)[R], int g, RowFn& rowof) {
+#pragma unroll
+  for (int i = 0; i < R; ++i) row[i] = rowof(g, i);
+}
+template <int R>
+__device__ __forceinline__ void slice_load(u32x4 (&b)[R], const int (&row)[R], const uint16_t* __restrict__ W, int K, int j) {
+  const int nchunk = K >> 3;
+  const int c = lane_id() + 64 * j;
+  const int cc = c < nchunk ? c : nchunk - 1;
+  int first = row[0];
+#pragma unroll
+  for (int i = 1; i < R; ++i)
+    if (first < 0) first = row[i];
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    const int r = row[i] >= 0 ? row[i] : first;
+    b[i] = ldw16(W + (size_t)r * K + (size_t)cc * 8);
+  }
+  fx_issue_here();
+}
+template <int R, int NJ, int D, class RowFn>
+__device__ __forceinline__ void slices_prime(SliceRing<R, D>& q, const uint16_t* W, int K, int ngroups, RowFn& rowof) {
+  if (wave_id() >= ngroups) return;
+  slice_rows(q.row, wave_id(), rowof);
+#pragma unroll
+  for (int d = 0; d < D && d < NJ; ++d) slice_load(q.w[d], q.row, W, K, d);
+}
+template <int NJ, int WS = FX_WAVES, int R, int D, class RowFn, class XsFn, class EmitFn>
+__device__ __forceinline__ void gemv_slices_x(SliceRing<R, D>& q, const uint16_t* W, int K, XsFn xsof, int ngroups,
+                                              RowFn& rowof, EmitFn emit) {
+  static_assert(NJ % D == 0, "a group's slices must fill the ring evenly");
+  const int nchunk = K >> 3;
+  int g = wave_id();
+  int rown[R];
+  while (g < ngroups) {
+    const int gn = g + WS;
+    if (gn < ngroups) slice_rows(rown, gn, rowof);
+    const float* xs = xsof(g);
+    float acc[R];
+#pragma unroll
+    for (int i = 0; i < R; ++i) acc[i] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const int c = lane_id() + 64 * j;
+      if (c < nchunk) {
+        const float4* xp = (const float4*)(xs + c * 8);
+        const float4 a = xp[0], b = xp[1];
+        const float xv[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+        for (int i = 0; i < R; ++i) acc[i] = fma8(q.w[j % D][i], xv, acc[i]);
+      }
+      // refill the slice just consumed with the one D places further on
+      if (j + D < NJ) slice_load(q.w[j % D], q.row, W, K, j + D);
+      else if (gn < ngroups) slice_load(q.w[j % D], rown, W, K, j + D - NJ);
+    }
+    if (nchunk >= 64) {
+#pragma unroll
+      for (int i = 0; i < R; ++i) acc[i] = butterfly64(acc[i]);
+    } else {
+      const int nl = lanes_for(nchunk);
+#pragma unroll
+      for (int i = 0; i < R; ++i) acc[i] = butterfly(acc[i], nl);
+    }
+    emit(g, q.row, acc);
+    if (gn >= ngroups) break;
+#pragma unroll
+    for (int i = 0; i < R; ++i) q.row[i] = rown[i];
+    g = gn;
+  }
+}
+
+// A GEMV stage's walk over its groups: the tiled pipeline (two whole tiles in flight per wave), or,
+// built with FX_SLICE_D > 0, for the K = 2048 bf16 tiles the sliced one (FX_SLICE_D slices of 4 KiB
+// in flight per wave). Same arithmetic either way. The sliced walk streams as fast as the tiled one
+// on its own (harness/probes.py --gemv) but made the decode slower (1,696 / 1,703 against 1,680 /
+// 1,674 us per token at ctx 1,024), so the default is the tiled walk.
+#ifndef FX_SLICE_D
+#define FX_SLICE_D 0
+#endif
+template <class TileT>
+struct Walker {
+  TileT t0;
+  template <class WT, class RowFn>
+  __device__ __forceinline__ void prime(const WT& W, int K, int ngroups, RowFn& rowof) {
+    gemv_prime(t0, W, K, ngroups, rowof);
+  }
+  template <class WT, class RowFn, class EmitFn>
+  __device__ __forceinline__ void run(const WT& W, int K, const float* xs, int ngroups, RowFn& rowof, EmitFn emit) {
+    gemv_pipe(t0, W, K, xs, ngroups, rowof, emit);
+  }
+};
+#if FX_SLICE_D > 0
+template <>
+struct Walker<Tile<4, 4>> {
+  SliceRing<4, FX_SLICE_D> q;
+  template <class RowFn>
+  __device__ __forceinline__ void prime(const uint16_t* W, int K, int ngroups, RowFn& rowof) {
+    slices_prime<4, 4>(q, W, K, ngroups, rowof);
+  }
+  template <class RowFn, class EmitFn>
+  __device__ __forceinline__ void run(const uint16_t* W, int K, const float* xs, int ngroups, RowFn& rowof, EmitFn emit) {
+    gemv_slices_x<4>(q, W, K, [=](int) { return xs; }, ngroups, rowof, emit);
+  }
+};
+#endif
+
 // ------------------------------------------------------------------------------------------------
 // input-row prologues: every thread takes 8-element chunks i = 8 * tid, 8 * (tid + 256), ...
 
@@ -437,8 +554,8 @@ __device__ __forceinline__ void op_gemv_w(const fx_stage& s, FxEnv& env, const W
   const int r0 = g0 * 4, r1 = g1 * 4 < s.n_rows ? g1 * 4 : s.n_rows;
   const int ngroups = (r1 - r0 + R - 1) / R;
   auto rowof = [&](int g, int i) { const int r = r0 + g * R + i; return r < r1 ? r : -1; };
-  TileT t0;
-  gemv_prime(t0, W, K, ngroups, rowof);
+  Walker<TileT> wk;
+  wk.prime(W, K, ngroups, rowof);
   const bool norm = (s.flags & FX_F_NORM) != 0;
   const NormW nw = norm && K <= 8 * FX_THREADS ? norm_prefetch((const uint16_t*)s.w_norm, K) : NormW{};
   const bool out_ll = (s.flags & FX_F_OUT_LL) != 0;
@@ -475,7 +592,7 @@ __device__ __forceinline__ void op_gemv_w(const fx_stage& s, FxEnv& env, const W
   const bool add_res = residual || res_embed;
   float best = -__builtin_inff();
   int best_i = 0x7fffffff;
-  gemv_pipe(t0, W, K, xs, ngroups, rowof, [&](int g, const int* row, const float* acc) {
+  wk.run(W, K, xs, ngroups, rowof, [&](int g, const int* row, const float* acc) {
     const int lane = lane_id();
 #pragma unroll
     for (int i = 0; i < R; ++i) {

@@ -9,7 +9,7 @@
 
 #include <vector>
 
-#include "fx_device.h"
+#include "fx_gemv.h"
 
 #define PROBE_LIMIT (100ull * 1000 * 1000)   // 1 s of s_memrealtime ticks: every wait gives up after it
 
@@ -417,6 +417,74 @@ __global__ void __launch_bounds__(256) fxp_loaded_kernel(uint32_t* flag, int a, 
   else loaded_stream<24>(base, per, &flag[64], bytes_out, ticks_out, work);
 }
 
+// ---- the decode GEMV's own walk (fx_gemv.h: Tile<4, 4> over K = 2048, double-buffered, groups of 4
+// rows, wave w taking groups w, w + 4, ...) over `rows_per_block` rows per block of W, timed.
+// mode 0: tile_dot (the real dot_lanes work); mode 1: the same loads, each tile folded by one xor
+// per word (no dot); mode 2: as 1 with every load instruction of a tile reading the next KiB of the
+// tile's 16 contiguous KiB (instead of row-interleaved); modes 3, 4: the sliced walk (gemv_slices_x)
+// with 2 / 4 slices (4 rows x 1 KiB) in flight per wave.
+template <int MODE>
+__device__ __forceinline__ void gemv_walk(const uint16_t* W, int K, int r0, int ngroups, const float* xs, float& sink) {
+  auto rowof = [&](int g, int i) { return r0 + g * 4 + i; };
+  if constexpr (MODE == 0) {
+    Tile<4, 4> t0;
+    gemv_prime(t0, W, K, ngroups, rowof);
+    gemv_pipe(t0, W, K, xs, ngroups, rowof, [&](int, const int*, const float* acc) { sink += acc[0] + acc[1] + acc[2] + acc[3]; });
+  } else if constexpr (MODE >= 3) {
+    // the sliced walk with 2 (mode 3) or 4 (mode 4) slices of 4 KiB in flight per wave
+    constexpr int D = MODE == 3 ? 2 : 4;
+    SliceRing<4, D> q;
+    slices_prime<4, 4>(q, W, K, ngroups, rowof);
+    gemv_slices_x<4>(q, W, K, [&](int) { return xs; }, ngroups, rowof,
+                     [&](int, const int*, const float* acc) { sink += acc[0] + acc[1] + acc[2] + acc[3]; });
+  } else {
+    auto load = [&](u32x4* v, int g) {
+      const uint8_t* base = (const uint8_t*)(W + (size_t)(r0 + g * 4) * K);
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int kib = MODE == 1 ? i * 4 + j : j * 4 + i;
+          v[j * 4 + i] = *(const u32x4*)__builtin_assume_aligned(base + (size_t)kib * 1024 + lane_id() * 16, 16);
+        }
+    };
+    uint32_t acc = 0;
+    u32x4 a[16], b[16];
+    int g = wave_id();
+    if (g < ngroups) load(a, g);
+    while (g < ngroups) {
+      const int g1 = g + FX_WAVES;
+      if (g1 < ngroups) load(b, g1);
+#pragma unroll
+      for (int k = 0; k < 16; ++k) acc ^= a[k].x ^ a[k].y ^ a[k].z ^ a[k].w;
+      if (g1 >= ngroups) break;
+      const int g2 = g1 + FX_WAVES;
+      if (g2 < ngroups) load(a, g2);
+#pragma unroll
+      for (int k = 0; k < 16; ++k) acc ^= b[k].x ^ b[k].y ^ b[k].z ^ b[k].w;
+      g = g2;
+    }
+    sink += (float)(acc & 1u);
+  }
+}
+__global__ void __launch_bounds__(256) fxp_gemv_kernel(const uint16_t* W, int K, int rows_per_block, int mode,
+                                                       uint64_t* ticks, float* out) {
+  __shared__ float xs[2048];
+  for (int i = threadIdx.x; i < K; i += 256) xs[i] = 0.001f * (float)(i % 7);
+  __syncthreads();
+  const int r0 = blockIdx.x * rows_per_block, ngroups = rows_per_block / 4;
+  float sink = 0.0f;
+  const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+  if (mode == 0) gemv_walk<0>(W, K, r0, ngroups, xs, sink);
+  else if (mode == 1) gemv_walk<1>(W, K, r0, ngroups, xs, sink);
+  else if (mode == 2) gemv_walk<2>(W, K, r0, ngroups, xs, sink);
+  else if (mode == 3) gemv_walk<3>(W, K, r0, ngroups, xs, sink);
+  else gemv_walk<4>(W, K, r0, ngroups, xs, sink);
+  __syncthreads();
+  if (threadIdx.x == 0) ticks[blockIdx.x] = __builtin_amdgcn_s_memrealtime() - t0;
+  if (sink == 1234.5f) out[0] = sink;
+}
+
 // ---- lane exchange check: out[lane * 6 + k] = the value xor_lane<2^k> returns on `lane` when every
 // lane holds its own index (must be lane ^ 2^k)
 // ---- FP8 decode: the 256 codes through the hardware's packed FP8 -> f32 conversion (lane l: codes
@@ -729,6 +797,32 @@ int fxp_loaded(int a, int b, uint32_t rounds, int depth, int work, const void* l
   (void)hipFree(bo);
   (void)hipFree(to);
   return 0;
+}
+
+// the GEMV walk over rows_per_block * blocks rows of W [rows][K] (K = 2048, rows_per_block a multiple
+// of 4): per-block ticks and the launch's event time
+int fxp_gemv(const void* W, int K, int rows_per_block, int blocks, int mode, uint64_t* ticks_host, float* ms) {
+  if (K != 2048 || rows_per_block % 4 || mode < 0 || mode > 4 || blocks <= 0) return -1;
+  uint64_t* d_ticks = nullptr;
+  float* out = nullptr;
+  hipEvent_t e0, e1;
+  hipError_t e;
+  if ((e = hipMalloc(&d_ticks, 8 * blocks)) != hipSuccess) return e;
+  if ((e = hipMalloc(&out, 64)) != hipSuccess) return e;
+  (void)hipEventCreate(&e0);
+  (void)hipEventCreate(&e1);
+  (void)hipEventRecord(e0, 0);
+  hipLaunchKernelGGL(fxp_gemv_kernel, dim3(blocks), dim3(256), 0, 0, (const uint16_t*)W, K, rows_per_block, mode,
+                     d_ticks, out);
+  (void)hipEventRecord(e1, 0);
+  if ((e = hipEventSynchronize(e1)) != hipSuccess) return e;
+  (void)hipEventElapsedTime(ms, e0, e1);
+  e = hipMemcpy(ticks_host, d_ticks, 8 * blocks, hipMemcpyDeviceToHost);
+  (void)hipFree(d_ticks);
+  (void)hipFree(out);
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  return e;
 }
 
 int fxp_dot2(const uint32_t* a_host, const uint32_t* b_host, const float* c_host, float* d_host, int n) {

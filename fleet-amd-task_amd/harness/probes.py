@@ -34,6 +34,8 @@ def probe_lib():
                                ctypes.POINTER(u64)]
     L.fxp_loaded.argtypes = [ctypes.c_int, ctypes.c_int, u32, ctypes.c_int, ctypes.c_int, vp, u64, ctypes.c_int,
                              ctypes.c_int, ctypes.POINTER(u64)]
+    L.fxp_gemv.argtypes = [vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.POINTER(u64),
+                           ctypes.POINTER(ctypes.c_float)]
     L.fxp_lanes.argtypes = [ctypes.POINTER(ctypes.c_float)]
     L.fxp_valu.argtypes = [ctypes.POINTER(u64)]
     L.fxp_icache.argtypes = [vp, u64, ctypes.POINTER(u64)]
@@ -61,6 +63,8 @@ def main():
     ap.add_argument("--clock", action="store_true")
     ap.add_argument("--pingpong-only", action="store_true", help="only the flag round trips")
     ap.add_argument("--valu", action="store_true", help="only the VALU issue rate of FMA chains")
+    ap.add_argument("--gemv", action="store_true",
+                    help="only the decode GEMV walk (Tile<4, 4>, K = 2048) against the same loads without the dot")
     ap.add_argument("--loaded", action="store_true",
                     help="only the sc1 flag round trip against the depth of a concurrent full-chip stream")
     ap.add_argument("--reuse", action="store_true",
@@ -103,6 +107,29 @@ def main():
             print(f"instruction fetch ({'under stream' if load else 'idle'}, launch {rep}): 4096 x 8-byte v_fmac_f32 "
                   f"straight-line, cold pass {oc[0]} cycles ({oc[0] / 4096:.2f}/instr), warm pass {oc[1]} cycles "
                   f"({oc[1] / 4096:.2f}/instr)", flush=True)
+        rt.close()
+        return
+    if args.gemv:
+        rows = 102400
+        W = rt.alloc((rows * 2048 * 2,), "u8")
+        # contents do not matter for the timing (uninitialised bf16 words)
+        cold = rt.alloc((1 << 30,), "u8")
+        ticks = (ctypes.c_uint64 * 256)()
+        ms = ctypes.c_float()
+        print("| walk | rows per block | MiB per block | GB/s (events) | median us/block | max us/block |", flush=True)
+        print("|---|---|---|---|---|---|", flush=True)
+        names = {0: "tile_dot (decode GEMV)", 1: "same loads, xor only", 2: "contiguous KiB order, xor only",
+                 3: "sliced, 2 slices in flight", 4: "sliced, 4 slices in flight"}
+        for rpb in (400, 100, 36):
+            for mode in (0, 3, 4, 1):
+                for rep in range(2):
+                    # evict W from the last-level cache between timed walks
+                    assert L.fxp_stream(ctypes.c_void_p(cold.ptr), cold.nbytes // 256, 256, 256, 8, 0, ticks, ctypes.byref(ms)) == 0
+                    assert L.fxp_gemv(ctypes.c_void_p(W.ptr), 2048, rpb, 256, mode, ticks, ctypes.byref(ms)) == 0
+                t = np.array(ticks[:256], np.float64) * TICK_NS / 1e3
+                nb = rpb * 2048 * 2
+                print(f"| {names[mode]} | {rpb} | {nb / 2**20:.2f} | {256 * nb / (ms.value * 1e6):.0f} | "
+                      f"{np.median(t):.2f} | {t.max():.2f} |", flush=True)
         rt.close()
         return
     if args.loaded:
