@@ -161,14 +161,14 @@ def default_splits(s_max, attn="mfma"):
     valu, xcd: the fewest 32-position tiles per split that keep every split on its own worker of an
     XCD (at most 32 splits), so the attention runs in one round and the merge reads at most 32
     partials per head.
-    mfma: one split per worker and every head per split, so the splits are short: 32 positions up
-    to 32 splits, then as many positions as keep the split count at most 64 (the merge reads every
-    live split's partial for its head)."""
+    mfma: one split per worker and every head per split, so the splits are short: 32 positions per
+    4,096 of the cache (rounded to the nearest multiple; at least 32), i.e. about 128 splits once the
+    cache passes 4,096 positions. Measured at ctx 16,384 on MI355X (us/token): split 64 (257 splits)
+    2,704, 96 2,490, 128 2,381, 160 2,396, 192 2,433, 288 (57 splits) 2,611; at ctx 1,024 the 33
+    splits of 32."""
     if attn in ("valu", "xcd"):
         return splits_for(s_max, n_splits=XWORKERS)
-    if -(-s_max // SPLIT) <= 32:
-        return splits_for(s_max, SPLIT)
-    return splits_for(s_max, n_splits=64)
+    return splits_for(s_max, SPLIT * max(1, round(s_max / 4096)))
 
 
 def build_plan(dims: Dims = REAL_DIMS, s_max: int = 1056, layers: int = 27, head: bool = True, split: int = None,

@@ -47,7 +47,9 @@ def test_plan_counts_and_chain():
     assert (G.build_plan(attn="valu").split, G.build_plan(attn="valu").n_splits) == (64, 17)
     xc = G.build_plan(attn="xcd")
     assert (xc.attn, xc.split, xc.n_splits) == ("xcd", 64, 17)
-    assert G.default_splits(16416) == (288, 57)
+    # beyond 4,096 positions about 128 splits (32 positions per 4,096 of the cache)
+    assert G.default_splits(16416) == (128, 129)
+    assert G.default_splits(4096) == (32, 128)
     assert (G.build_plan(split=32).split, G.build_plan(split=32).n_splits) == (32, 33)
     t = G.build_plan().truncate("L1.o_proj")
     assert t.calls[-1].label == "L1.o_proj"
