@@ -26,10 +26,12 @@ FIXTURE = os.path.join(os.path.dirname(__file__), "golden", "numpy_ref_decode.js
 ROUTER_TIE = 0.05
 
 
-@pytest.fixture(scope="module")
-def decoded():
+@pytest.fixture(scope="module", params=["mfma", "valu"])
+def decoded(request):
+    """The oracle's decode in the order of each attention kernel: the matrix-core one (the default
+    plan's) and the vector-ALU one; both must give numpy_ref's discrete outputs."""
     g = json.load(open(FIXTURE))
-    c = Cfg(split=g["split"], n_splits=g["s_max"] // g["split"])
+    c = Cfg(split=g["split"], n_splits=g["s_max"] // g["split"], attn=request.param)
     W = SeededCpuWeights(P.REAL_DIMS, g["seed"], g["layers"], head=True)
     cos, sin = rope_tables(g["s_max"], c.D_R)
     cache = Cache(c, g["s_max"], g["layers"])
