@@ -247,12 +247,16 @@ def _attention64(ql, qp, ck, kp, step, scale):
     return p @ fb(ck[:step + 1]).astype(np.float64)
 
 
-@pytest.mark.parametrize("S,step,split", [(64, 40, 32), (1056, 1023, 32), (300, 299, 100), (4096, 4095, 128)])
-def test_mla_attend_merge_vs_brute_force(S, step, split):
+@pytest.mark.parametrize("attn", ["valu", "mfma"])
+@pytest.mark.parametrize("S,step,split", [(64, 40, 32), (1056, 1023, 32), (300, 299, 96), (4096, 4095, 128)])
+def test_mla_attend_merge_vs_brute_force(S, step, split, attn):
+    """Both attention orders (the vector-ALU chains, mla_attend; the matrix-core instruction's,
+    mla_attend_mfma) against float64 softmax attention."""
     rng = np.random.default_rng(6 + S)
     ql, qp, ck, kp = _attn_inputs(rng, S)
     scale = float(F32(1 / np.sqrt(192)))
-    part = O.mla_attend(ql, qp, ck, kp, step, scale, split=split)
+    attend = O.mla_attend if attn == "valu" else O.mla_attend_mfma
+    part = attend(ql, qp, ck, kp, step, scale, split=split)
     n_splits = -(-S // split)
     live = -(-(step + 1) // split)
     assert part.shape == (n_splits, 16, 516)
@@ -264,9 +268,28 @@ def test_mla_attend_merge_vs_brute_force(S, step, split):
     ref_attn = np.einsum("hc,hvc->hv", fb(obf).astype(np.float64), fb(W_uv).astype(np.float64)).reshape(-1)
     assert _close_bf16(attn, ref_attn)
     # one split over everything equals many splits up to FP32 / bf16(p) rounding (test_numpy_ref.py:145-148)
-    one = O.mla_attend(ql, qp, ck, kp, step, scale, split=S)
-    attn1, _ = O.mla_merge_uv(one, W_uv, step, split=S)
+    S1 = -(-S // 32) * 32
+    one = attend(ql, qp, ck, kp, step, scale, split=S1)
+    attn1, _ = O.mla_merge_uv(one, W_uv, step, split=S1)
     assert np.linalg.norm(fb(attn1) - fb(attn)) / np.linalg.norm(fb(attn)) < 1e-2
+
+
+def test_mla_attend_mfma_exact_case():
+    """With q = 0 every score is 0 and every probability 1, so each split's partial is the plain
+    mean of its value rows and its lse is log(rows): with small dyadic cache values every sum is
+    exact in any order, and the matrix-core attention's partials equal the vector-ALU chains' bit
+    for bit (a wrong position or column in the value products would move an element)."""
+    rng = np.random.default_rng(11)
+    S, step = 96, 80
+    ql, qp = bf(np.zeros((16, 512))), bf(np.zeros((16, 64)))
+    ck = bf(rng.integers(-8, 9, (S, 512)) * 2.0 ** -6)
+    kp = bf(rng.integers(-8, 9, (S, 64)) * 2.0 ** -6)
+    pm = O.mla_attend_mfma(ql, qp, ck, kp, step, 0.125, split=32)
+    pv = O.mla_attend(ql, qp, ck, kp, step, 0.125, split=32)
+    assert np.array_equal(pm.view(np.uint32), pv.view(np.uint32))
+    for j in range((step + 1) // 32):   # the full splits: the mean of 32 rows is exact
+        rows = fb(ck[32 * j:32 * j + 32]).astype(np.float64)
+        assert np.array_equal(pm[j, 3, :512].astype(np.float64), rows.mean(axis=0))
 
 
 def test_mla_scores_and_lse():
