@@ -24,20 +24,23 @@ def oracle_cfg(plan, layers):
 
 
 def _run_model(rt, layers, n_prompt, n_new, s_max, attn, seed=SEED):
+    """attn: the plan's attention, with "-nopair" for o_proj and the gate|up stage as two operators."""
+    pair = not attn.endswith("-nopair")
+    attn = attn.split("-")[0]
     d = P.REAL_DIMS
     bufs = P.fill_seeded(rt, d, seed, layers=layers, head=True)
     prompt = P.prompt_ids(seed, n_prompt, d.V)
-    plan = G.build_plan(d, s_max, layers, True, attn=attn)
+    plan = G.build_plan(d, s_max, layers, True, attn=attn, pair=pair)
     meta = B.make_meta(rt, s_max, prompt)
     cap = B.make_capture(rt, plan)
-    runner = B.build(rt, bufs, cap, meta, d, s_max, layers, True, attn=attn)
-    print(f"[model] attn={attn} layers={layers} n_prompt={n_prompt} n_new={n_new} stages={len(runner.stages)}",
-          flush=True)
+    runner = B.build(rt, bufs, cap, meta, d, s_max, layers, True, attn=attn, pair=pair)
+    print(f"[model] attn={attn} pair={pair} layers={layers} n_prompt={n_prompt} n_new={n_new} "
+          f"stages={len(runner.stages)}", flush=True)
     runner.run(n_prompt - 1 + n_new, 0, n_prompt)
     return d, bufs, prompt, plan, runner, cap
 
 
-@pytest.mark.parametrize("attn", ["mfma", "xcd", "valu"])
+@pytest.mark.parametrize("attn", ["mfma", "mfma-nopair", "xcd", "valu"])
 @pytest.mark.parametrize("layers,n_prompt,n_new", [(2, 40, 4), (3, 70, 3)])
 def test_decode_matches_oracle(rt, layers, n_prompt, n_new, attn):
     s_max = 96
