@@ -632,6 +632,86 @@ __device__ __forceinline__ void merge_head(const void* part, int nh, int h, int 
   xs[pc + 1] = bf16r(num[1] / den);
 }
 
+// The same merge for long caches, by the 8 workers of a head on one XCD (matrix-core attention,
+// more than MERGE_BATCH live splits): worker v of the head merges columns [64 v, 64 v + 64) only.
+// Its 64-column slices of every live split's partial come into LDS with direct-to-LDS loads, all
+// requested at once (one round trip instead of one per MERGE_BATCH splits, and an eighth of the
+// bytes per worker); column c is then num = sum_j w_j o_j[c] in j order (fma) / den, the same
+// arithmetic as merge_head. The 8 slices are exchanged as XCD-local packets (opk, [nh][d_c] pk16,
+// tag `tag`) and xs[0, d_c) receives the whole head; ends with a barrier, as every thread then reads
+// columns other threads wrote.
+#define MERGE_SLICE_COLS 64
+#define MERGE_SLICE_MAX 160   // live splits whose slices fit below LDS_RED (4 per KiB)
+#define MERGE_SLICE_LDS 4096  // the slices' LDS, past xs's d_c floats
+static_assert(LDS_XS + MERGE_SLICE_LDS + MERGE_SLICE_MAX / 4 * 1024 <= LDS_RED, "merge slices overlap the reductions");
+__device__ __forceinline__ void merge_head_sliced(const void* part, int nh, int h, int prow, int d_c, int live, int v,
+                                                  float* xs, float* wj, float* red, void* opk, uint32_t tag,
+                                                  const FxEnv& env) {
+  char* land = env.lds + LDS_XS + MERGE_SLICE_LDS;
+  // wave 0: the lse of splits lane, lane + 64 first (loads complete in issue order)
+  float l0 = -__builtin_inff(), l1 = -__builtin_inff();
+  if (wave_id() == 0) {
+    if (lane_id() < live) l0 = ldcf(part, (uint32_t)((lane_id() * nh + h) * prow + d_c));
+    if (lane_id() + 64 < live) l1 = ldcf(part, (uint32_t)(((lane_id() + 64) * nh + h) * prow + d_c));
+  }
+  // every wave: instruction k brings splits 4k .. 4k + 3 (16 lanes x 16 B each) to land + 1 KiB k
+  const int nins = (live + 3) >> 2;
+  const int lane = lane_id();
+  for (int k = wave_id(); k < nins; k += FX_WAVES) {
+    int j = 4 * k + (lane >> 4);
+    j = j < live ? j : live - 1;
+    const char* src = (const char*)part + ((size_t)(j * nh + h) * prow + MERGE_SLICE_COLS * v) * 4 + (lane & 15) * 16;
+    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
+                                     (__attribute__((address_space(3))) void*)(land + k * 1024), 16, 0, FX_SC1);
+  }
+  if (wave_id() == 0) {
+    float mx = fmaxf(l0, l1);
+    for (int j = lane + 128; j < live; j += 64) {
+      const float x = ldcf(part, (uint32_t)((j * nh + h) * prow + d_c));
+      wj[j] = x;
+      mx = fmaxf(mx, x);
+    }
+    mx = wave_max(mx);
+    float den = 0.0f;
+    for (int j0 = 0; j0 < live; j0 += 64) {
+      const int j = j0 + lane;
+      const float lse = j0 == 0 ? l0 : (j0 == 64 ? l1 : (j < live ? wj[j] : -__builtin_inff()));
+      const float w = j < live ? exp_s(lse - mx) : 0.0f;
+      if (j < live) wj[j] = w;
+      const int n = live - j0 < 64 ? live - j0 : 64;
+      for (int u = 0; u < n; ++u) den = den + __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), u));
+    }
+    if (lane == 0) red[0] = den;
+    prof_mark(env, 4);
+  }
+  wait_mem();
+  __syncthreads();
+  const int c0 = MERGE_SLICE_COLS * v;
+  if (fx_tid() < MERGE_SLICE_COLS) {
+    const float* P = (const float*)land + fx_tid();
+    float num = 0.0f;
+    for (int j = 0; j < live; ++j) num = __builtin_fmaf(wj[j], P[j * MERGE_SLICE_COLS], num);
+    xs[c0 + fx_tid()] = bf16r(num / red[0]);
+  }
+  prof_mark(env, 6);
+  __syncthreads();
+  if (fx_tid() < MERGE_SLICE_COLS / 4) {
+    const float* r = xs + c0 + 4 * fx_tid();
+    pk_put2(opk, (uint32_t)((h * d_c + c0) / 2 + 2 * fx_tid()), pack2(r[0], r[1]), pack2(r[2], r[3]), tag, true);
+  }
+  // the head's d_c / 4 pairs of packets from its 8 workers (this one's included)
+  if (fx_tid() < (d_c >> 2)) {
+    u32x4 w[1];
+    const int q = (h * d_c >> 2) + fx_tid();
+    pk_wait_pairs<1>(opk, q, 0, q + 1, tag, env.err, w);
+    xs[4 * fx_tid() + 0] = bf_lo(w[0].x);
+    xs[4 * fx_tid() + 1] = bf_hi(w[0].x);
+    xs[4 * fx_tid() + 2] = bf_lo(w[0].z);
+    xs[4 * fx_tid() + 3] = bf_hi(w[0].z);
+  }
+  __syncthreads();
+}
+
 // FX_OP_MLA_MERGE_UV: ranks 0..15 / 16..31 of XCD x merge head 2x / 2x + 1 (merge_head), then
 // attn[h*d_v + v] = bf16(dot(o, W_uv[h][v])) for 8 rows v each (harness/numpy_ref.py:168-174).
 // With FX_F_MFMA the merge runs on ranks 16..31 of every XCD only (workers 128..255), 8 per head
@@ -671,7 +751,12 @@ __device__ __forceinline__ void op_mla_merge_uv(const fx_stage& s, FxEnv& env) {
   }
   __syncthreads();
   prof_mark(env, 1);
-  merge_head((const void*)s.x, nh, h, prow, d_c, live, xs, (float*)(env.lds + LDS_TILE), red, env);
+  const bool sliced = mfma && s.aux[7] && live > MERGE_BATCH && live <= MERGE_SLICE_MAX;
+  if (sliced)
+    merge_head_sliced((const void*)s.x, nh, h, prow, d_c, live, mr % MERGE_MFMA_PER_HEAD, xs,
+                      (float*)(env.lds + LDS_TILE), red, (void*)s.aux[7], tag_out(env), env);
+  else
+    merge_head((const void*)s.x, nh, h, prow, d_c, live, xs, (float*)(env.lds + LDS_TILE), red, env);
   const int pc = fx_tid() * 2;
   if (v0 == 0 && s.aux[4]) stc4((void*)s.aux[4], (uint32_t)(h * d_c + pc) * 2, pack2(xs[pc], xs[pc + 1]));
   __syncthreads();

@@ -715,6 +715,9 @@ int fx_mla_attend_merge_noalloc(fx_ctx* c, const fx_stage* attend, const fx_stag
   a.aux[6] = done;
   m.x = part;
   m.aux[6] = done;
+  // no slice-exchange buffer: the merge reads every column itself (the exchange packets would be
+  // caller memory beyond this entry's inputs and outputs)
+  if (!(merge->flags & FX_F_XCD)) m.aux[7] = 0;
   // the merge waits for the attention's done packets; the single-XCD merge runs the attention itself
   // and waits for the attention's inputs
   const bool xcd = (merge->flags & FX_F_XCD) != 0;

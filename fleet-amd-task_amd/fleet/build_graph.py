@@ -152,6 +152,9 @@ def compile_stages(plan, host):
             ins = [(0, a["done"])]
             if plan.attn == "mfma":
                 st.flags |= R.FX_F_MFMA
+                # long caches: each of a head's 8 merge workers merges 64 columns and they exchange
+                # them through these packets
+                st.aux[7] = B(a.get("slices"))
             if plan.attn == "xcd":
                 # the attention and the merge on one XCD: the attention's operands in the spare fields
                 att = pend_attend

@@ -54,7 +54,7 @@ OUTPUT_ARGS = {
     "linear_gemv_layer": ["output", "amax"],
     "mla_prep_layer": ["c_kv", "k_pe", "ql_nope", "q_pe", "crow"],
     "mla_attend_layer": ["partials", "done"],
-    "mla_merge_uv_layer": ["output", "o_merged"],
+    "mla_merge_uv_layer": ["output", "o_merged", "slices"],
     "moe_router_layer": ["logits_x"],
     "gang_moe_w13_gemv_layer": ["output", "topk_w", "routing", "mask", "logits", "route_log", "h", "sel"],
     "gang_moe_w2_linear_layer": ["output"],
@@ -207,6 +207,7 @@ def build_plan(dims: Dims = REAL_DIMS, s_max: int = 1056, layers: int = 27, head
     p.t("partials", (n_splits, d.NH, partials_row(d.D_C)), "f32")
     p.t("att_done", (XCDS, XWORKERS), "pk32")
     p.t("o_merged", (d.NH, d.D_C))
+    p.t("o_slices", (d.NH, d.D_C), "pk16")   # merged o of each head, exchanged between its merge workers
     p.t("attn", (d.NH * d.D_V,), "pk16")
     p.t("cos", (s_max, d.D_R), kind="input", source="capture:cos")
     p.t("sin", (s_max, d.D_R), kind="input", source="capture:sin")
@@ -246,7 +247,8 @@ def build_plan(dims: Dims = REAL_DIMS, s_max: int = 1056, layers: int = 27, head
              c_kv=f"c_kv_{l}", k_pe=f"k_pe_{l}", partials="partials", done="att_done",
              softmax_scale=softmax_scale, split=split, n_splits=n_splits)
         p.op("mla_merge_uv_layer", WORKERS, f"L{l}.mla_merge_uv", input="partials", done="att_done",
-             w_uv=f"W_uv_{l}", output="attn", o_merged="o_merged", split=split, n_splits=n_splits)
+             w_uv=f"W_uv_{l}", output="attn", o_merged="o_merged", slices="o_slices", split=split,
+             n_splits=n_splits)
         p.op("linear_gemv_layer", WORKERS, f"L{l}.o_proj", input="attn", w_norm=None, weight=f"W_o_{l}",
              residual="x_res", output="x_mid", norm=False)
         if l == 0:

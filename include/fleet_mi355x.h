@@ -118,7 +118,9 @@ enum fx_op {
                             * v_mfma_f32_16x16x32_bf16); done(aux6) holds one packet per worker, the merge
                             * waits for workers 0 .. min(live splits, 256) - 1 and runs on ranks 16..31 of
                             * every XCD (workers 128..255): ranks 16..23 / 24..31 of XCD x take head 2x /
-                            * 2x + 1, 16 W_uv rows each */
+                            * 2x + 1, 16 W_uv rows each. MLA_MERGE_UV aux7 (optional, [n_rows][d_c] packets):
+                            * with 41..160 live splits each of a head's 8 workers merges 64 columns and
+                            * they exchange them there (XCD-local) before W_uv */
 
 #define FX_F_XLOCAL 1024u  /* MLA_PREP: every reader of its packets runs on the producing XCD (the VALU
                             * attention: XCD x owns heads 2x, 2x + 1), so they are stored XCD-local (sc0)

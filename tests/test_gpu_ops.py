@@ -239,13 +239,22 @@ def test_mla_attend_merge_uv(rt, attn, s_max, step, split):
     e_attn, e_obf = O.mla_merge_uv(exp, W_uv, step, split=split)
     attn = pk_out(rt, (NH * DN,))
     om = sentinel(rt, (NH, DC), "bf16")
+    # the matrix-core merge takes the slice-exchange packets (used beyond 40 live splits: each of a
+    # head's 8 workers merges 64 columns)
+    slices = pk_out(rt, (NH, DC)) if mfma else None
+    aux = {4: om.ptr, 6: done.ptr}
+    if mfma:
+        aux[7] = slices.ptr
     st = R.FxStage().set(op=R.FX_OP_MLA_MERGE_UV, flags=flags, n_rows=NH, d_c=DC, d_r=DR, d_n=DN, split=split,
                          n_splits=n_splits,
                          prow=prow, x=part.ptr, w=dev(rt, W_uv, "bf16").ptr, out=attn.ptr,
-                         aux={4: om.ptr, 6: done.ptr}, src=[SIDX, 0, 0, 0])
+                         aux=aux, src=[SIDX, 0, 0, 0])
     rt.run_stage(st, step=step, tbase=TB, sidx=SIDX + 1)
     assert mismatch(om.download(), e_obf) == 0
     assert mismatch(attn.download(tag=TOUT + 1), e_attn) == 0
+    if mfma and 40 < live <= 160:
+        # the exchanged slices are the merged o of every head, tagged by the merge stage
+        assert mismatch(slices.download(tag=TOUT + 1).reshape(NH, DC), e_obf) == 0
 
 
 XCD_POINTS = [(1056, 1023, 32),                     # 32 live splits: one per rank of the XCD
