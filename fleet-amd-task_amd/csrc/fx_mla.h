@@ -632,14 +632,17 @@ __device__ __forceinline__ void merge_head(const void* part, int nh, int h, int 
   xs[pc + 1] = bf16r(num[1] / den);
 }
 
-// The same merge for long caches, by the 8 workers of a head on one XCD (matrix-core attention,
-// more than MERGE_BATCH live splits): worker v of the head merges columns [64 v, 64 v + 64) only.
+// The same merge by the 8 workers of a head on one XCD (matrix-core attention, more than
+// MERGE_SLICE_MIN live splits): worker v of the head merges columns [64 v, 64 v + 64) only.
 // Its 64-column slices of every live split's partial come into LDS with direct-to-LDS loads, all
 // requested at once (one round trip instead of one per MERGE_BATCH splits, and an eighth of the
 // bytes per worker); column c is then num = sum_j w_j o_j[c] in j order (fma) / den, the same
 // arithmetic as merge_head. The 8 slices are exchanged as XCD-local packets (opk, [nh][d_c] pk16,
 // tag `tag`) and xs[0, d_c) receives the whole head; ends with a barrier, as every thread then reads
 // columns other threads wrote.
+#ifndef MERGE_SLICE_MIN
+#define MERGE_SLICE_MIN 8   // the sliced merge takes more live splits than this
+#endif
 #define MERGE_SLICE_COLS 64
 #define MERGE_SLICE_MAX 160   // live splits whose slices fit below LDS_RED (4 per KiB)
 #define MERGE_SLICE_LDS 4096  // the slices' LDS, past xs's d_c floats
@@ -751,7 +754,7 @@ __device__ __forceinline__ void op_mla_merge_uv(const fx_stage& s, FxEnv& env) {
   }
   __syncthreads();
   prof_mark(env, 1);
-  const bool sliced = mfma && s.aux[7] && live > MERGE_BATCH && live <= MERGE_SLICE_MAX;
+  const bool sliced = mfma && s.aux[7] && live > MERGE_SLICE_MIN && live <= MERGE_SLICE_MAX;
   if (sliced)
     merge_head_sliced((const void*)s.x, nh, h, prow, d_c, live, mr % MERGE_MFMA_PER_HEAD, xs,
                       (float*)(env.lds + LDS_TILE), red, (void*)s.aux[7], tag_out(env), env);

@@ -239,8 +239,8 @@ def test_mla_attend_merge_uv(rt, attn, s_max, step, split):
     e_attn, e_obf = O.mla_merge_uv(exp, W_uv, step, split=split)
     attn = pk_out(rt, (NH * DN,))
     om = sentinel(rt, (NH, DC), "bf16")
-    # the matrix-core merge takes the slice-exchange packets (used beyond 40 live splits: each of a
-    # head's 8 workers merges 64 columns)
+    # the matrix-core merge takes the slice-exchange packets (used from 9 to 160 live splits: each of
+    # a head's 8 workers merges 64 columns)
     slices = pk_out(rt, (NH, DC)) if mfma else None
     aux = {4: om.ptr, 6: done.ptr}
     if mfma:
@@ -252,7 +252,7 @@ def test_mla_attend_merge_uv(rt, attn, s_max, step, split):
     rt.run_stage(st, step=step, tbase=TB, sidx=SIDX + 1)
     assert mismatch(om.download(), e_obf) == 0
     assert mismatch(attn.download(tag=TOUT + 1), e_attn) == 0
-    if mfma and 40 < live <= 160:
+    if mfma and 8 < live <= 160:
         # the exchanged slices are the merged o of every head, tagged by the merge stage
         assert mismatch(slices.download(tag=TOUT + 1).reshape(NH, DC), e_obf) == 0
 
