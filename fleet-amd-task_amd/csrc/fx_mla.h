@@ -644,13 +644,14 @@ __device__ __forceinline__ void merge_head(const void* part, int nh, int h, int 
 #define MERGE_SLICE_MIN 8   // the sliced merge takes more live splits than this
 #endif
 #define MERGE_SLICE_COLS 64
-#define MERGE_SLICE_MAX 160   // live splits whose slices fit below LDS_RED (4 per KiB)
-#define MERGE_SLICE_LDS 4096  // the slices' LDS, past xs's d_c floats
-static_assert(LDS_XS + MERGE_SLICE_LDS + MERGE_SLICE_MAX / 4 * 1024 <= LDS_RED, "merge slices overlap the reductions");
+#define MERGE_SLICE_MAX 176                 // live splits whose slices fit (4 per KiB)
+#define MERGE_SLICE_LDS (LDS_TILE + 2048)   // the slices' LDS, past the weights wj[live] at LDS_TILE
+static_assert(MERGE_SLICE_LDS + MERGE_SLICE_MAX / 4 * 1024 <= LDS_STAGE, "merge slices overlap the stage LDS");
+static_assert(MERGE_SLICE_MAX * 4 <= 2048, "the merge weights overlap the slices");
 __device__ __forceinline__ void merge_head_sliced(const void* part, int nh, int h, int prow, int d_c, int live, int v,
                                                   float* xs, float* wj, float* red, void* opk, uint32_t tag,
                                                   const FxEnv& env) {
-  char* land = env.lds + LDS_XS + MERGE_SLICE_LDS;
+  char* land = env.lds + MERGE_SLICE_LDS;
   // wave 0: the lse of splits lane, lane + 64 first (loads complete in issue order)
   float l0 = -__builtin_inff(), l1 = -__builtin_inff();
   if (wave_id() == 0) {

@@ -119,7 +119,7 @@ enum fx_op {
                             * waits for workers 0 .. min(live splits, 256) - 1 and runs on ranks 16..31 of
                             * every XCD (workers 128..255): ranks 16..23 / 24..31 of XCD x take head 2x /
                             * 2x + 1, 16 W_uv rows each. MLA_MERGE_UV aux7 (optional, [n_rows][d_c] packets):
-                            * with 9..160 live splits each of a head's 8 workers merges 64 columns and
+                            * with 9..176 live splits each of a head's 8 workers merges 64 columns and
                             * they exchange them there (XCD-local) before W_uv */
 
 #define FX_F_XLOCAL 1024u  /* MLA_PREP: every reader of its packets runs on the producing XCD (the VALU

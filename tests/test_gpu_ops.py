@@ -185,7 +185,8 @@ def test_mla_prep(rt):
 ATTEND_POINTS = [(1056, 1023, 32), (1056, 1040, 32), (1056, 1024, 64), (4096, 4095, 128), (300, 40, 32), (64, 0, 32),
                  (32768, 32767, 1024), (16416, 16383, 160),
                  (8192, 4127, 32)]                  # 129 live splits: the merge's lse beyond 128 splits
-MFMA_POINTS = [(16416, 16383, 128),                 # exactly 128 live splits
+MFMA_POINTS = [(16416, 16383, 96),                  # 171 live splits, the sliced merge's most
+               (16416, 16383, 128),                 # exactly 128 live splits
                (16416, 16384, 128),                 # its next token: 129
                (8192, 8191, 32),                    # 256 live splits, one per worker
                (8448, 8447, 32)]                    # 264: workers 0..7 run two splits
@@ -239,7 +240,7 @@ def test_mla_attend_merge_uv(rt, attn, s_max, step, split):
     e_attn, e_obf = O.mla_merge_uv(exp, W_uv, step, split=split)
     attn = pk_out(rt, (NH * DN,))
     om = sentinel(rt, (NH, DC), "bf16")
-    # the matrix-core merge takes the slice-exchange packets (used from 9 to 160 live splits: each of
+    # the matrix-core merge takes the slice-exchange packets (used from 9 to 176 live splits: each of
     # a head's 8 workers merges 64 columns)
     slices = pk_out(rt, (NH, DC)) if mfma else None
     aux = {4: om.ptr, 6: done.ptr}
@@ -252,7 +253,7 @@ def test_mla_attend_merge_uv(rt, attn, s_max, step, split):
     rt.run_stage(st, step=step, tbase=TB, sidx=SIDX + 1)
     assert mismatch(om.download(), e_obf) == 0
     assert mismatch(attn.download(tag=TOUT + 1), e_attn) == 0
-    if mfma and 8 < live <= 160:
+    if mfma and 8 < live <= 176:
         # the exchanged slices are the merged o of every head, tagged by the merge stage
         assert mismatch(slices.download(tag=TOUT + 1).reshape(NH, DC), e_obf) == 0
 
