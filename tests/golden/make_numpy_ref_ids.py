@@ -8,7 +8,11 @@ its exact bits cannot be restated; its discrete outputs (token ids, expert ids) 
 script is run once, in the build container where the reference is checked out, and the JSON it
 writes is the committed fixture; nothing else imports the reference.
 
-    python tests/golden/make_numpy_ref_ids.py [/path/to/reference]
+    python tests/golden/make_numpy_ref_ids.py [/path/to/reference]            # numpy_ref_decode.json
+    python tests/golden/make_numpy_ref_ids.py --deep [/path/to/reference]     # numpy_ref_decode_27.json
+
+--deep: all 27 layers (26 MoE), the same 40-token prompt and 6 decoded tokens, without the
+per-layer hidden rows (ids, route ids, logit gaps and the final hidden row only).
 """
 import importlib.util
 import json
@@ -46,7 +50,12 @@ def f32(bits):
 
 
 def main():
-    ref_root = sys.argv[1] if len(sys.argv) > 1 else "/root/reference"
+    global LAYERS, N_NEW
+    args = [a for a in sys.argv[1:] if not a.startswith("--")]
+    deep = "--deep" in sys.argv
+    if deep:
+        LAYERS, N_NEW = P.REAL_DIMS.L, 6
+    ref_root = args[0] if args else "/root/reference"
     nr = load_numpy_ref(ref_root)
     c = Cfg(split=SPLIT, n_splits=S_MAX // SPLIT)
     W = SeededCpuWeights(P.REAL_DIMS, SEED, LAYERS, head=True)
@@ -111,7 +120,9 @@ def main():
         _, logits = nr.linear_norm(x, w("w_final_norm"), w("W_lm"), eps=c.eps)
         tok = int(np.argmax(logits))
         srt = np.sort(logits)[::-1]
-        return {"id": tok, "gap_1_2": float(srt[0] - srt[1])}, routes, x
+        top = [int(i) for i in np.argsort(-logits, kind="stable")[:3]]
+        return {"id": tok, "gap_1_2": float(srt[0] - srt[1]), "top3": top,
+                "top3_logits": [float(logits[i]) for i in top]}, routes, x
 
     for pos in range(N_PROMPT - 1):
         step_fn(prompt[pos], pos, False)
@@ -120,10 +131,15 @@ def main():
     x = None
     for i in range(N_NEW):
         step = N_PROMPT - 1 + i
-        hidden = []
+        hidden = None if deep else []
         t, routes, x = step_fn(tok, step, True, hidden)
-        steps.append({"step": step, "token": t["id"], "logit_gap_1_2": t["gap_1_2"], "routes": routes,
-                      "hidden_bf16": hidden})
+        rec = {"step": step, "token": t["id"], "logit_gap_1_2": t["gap_1_2"], "routes": routes}
+        if deep:
+            rec["top3"], rec["top3_logits"] = t["top3"], t["top3_logits"]
+        if not deep:
+            rec["hidden_bf16"] = hidden
+        steps.append(rec)
+        print(f"step {step}: token {t['id']} gap {t['gap_1_2']:.4g}", flush=True)
         tok = t["id"]
     out = {
         "what": "greedy decode by harness/numpy_ref.py operators on seeded synthetic weights",
@@ -131,8 +147,9 @@ def main():
         "scale": c.scale, "prompt": prompt, "steps": steps,
         "x_final_bf16": [int(v) for v in O.f32_to_bf16(x)],
     }
-    with open(os.path.join(HERE, "numpy_ref_decode.json"), "w") as f:
-        json.dump(out, f, indent=1)
+    name = "numpy_ref_decode_27.json" if deep else "numpy_ref_decode.json"
+    with open(os.path.join(HERE, name), "w") as f:
+        json.dump(out, f, indent=None if deep else 1)
     print(json.dumps([{k: s[k] for k in ("step", "token", "logit_gap_1_2")} for s in steps]))
 
 
