@@ -162,14 +162,188 @@ __device__ __forceinline__ void gemv_prime(TileT& t0, const WT& W, int K, int ng
   if (wave_id() < ngroups) tile_load(t0, W, K, wave_id(), rowof);
 }
 
+// The rolling walk: tile_dot of group k that, as soon as chunk column j of every row has been
+// consumed, re-fills those registers with chunk j of group gn (the wave's group two tiles ahead),
+// so the next tile's loads leave during this dot instead of after it, with no more registers than
+// two tiles. Each row's dot is tile_dot's (chunks in increasing j, one fma per element, the same
+// butterfly); a lane past the row's last chunk computes on the last chunk and keeps its sum
+// unchanged (a select, not a branch: the loads are unconditional, so the compiler's load counters
+// stay exact). `rows` receives the reduced group's rows; t then describes group gn.
+__device__ __forceinline__ void roll_fence(float* acc, int n) {
+  // the chunk's fmas are complete before the loads that reuse its registers are issued
+  for (int i = 0; i < n; ++i) asm volatile("" : "+v"(acc[i])::"memory");
+}
+template <int R, int NJ, class RowFn>
+__device__ __forceinline__ void tile_dot_roll(Tile<R, NJ>& t, const float* xs, int K, float* acc, int* rows,
+                                              const uint16_t* __restrict__ W, int gn, RowFn& rowof) {
+  const int lane = lane_id();
+  const int nchunk = K >> 3;
+  int nrow[R];
+  int first = -1;
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    rows[i] = t.row[i];
+    nrow[i] = rowof(gn, i);
+    if (first < 0 && nrow[i] >= 0) first = nrow[i];
+    acc[i] = 0.0f;
+  }
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const int c = lane + 64 * j;
+    const bool on = c < nchunk;
+    const int cc = on ? c : nchunk - 1;
+    const float4* xp = (const float4*)(xs + cc * 8);
+    const float4 a = xp[0], b = xp[1];
+    const float xv[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+      const float v = fma8(t.w[i][j], xv, acc[i]);
+      acc[i] = on ? v : acc[i];
+    }
+    roll_fence(acc, R);
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+      const int r = nrow[i] >= 0 ? nrow[i] : first;
+      t.w[i][j] = ldw16(W + (size_t)r * K + (size_t)cc * 8);
+    }
+    fx_issue_here();
+  }
+#pragma unroll
+  for (int i = 0; i < R; ++i) t.row[i] = nrow[i];
+  if (nchunk >= 64) {
+#pragma unroll
+    for (int i = 0; i < R; ++i) acc[i] = butterfly64(acc[i]);
+  } else {
+    const int nl = lanes_for(nchunk);
+#pragma unroll
+    for (int i = 0; i < R; ++i) acc[i] = butterfly(acc[i], nl);
+  }
+}
+template <int R, int NJ, class RowFn>
+__device__ __forceinline__ void tile_dot_roll(TileQ<R, NJ>& t, const float* xs, int K, float* acc, int* rows,
+                                              const Fp8W& W, int gn, RowFn& rowof) {
+  const int lane = lane_id();
+  const int nchunk = K >> 4;
+  int nrow[R];
+  int first = -1;
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    rows[i] = t.row[i];
+    nrow[i] = rowof(gn, i);
+    if (first < 0 && nrow[i] >= 0) first = nrow[i];
+    acc[i] = 0.0f;
+  }
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const int c = lane + 64 * j;
+    const bool on = c < nchunk;
+    const int cc = on ? c : nchunk - 1;
+    const float4* xp = (const float4*)(xs + cc * 16);
+    const float4 a = xp[0], b = xp[1], e = xp[2], f = xp[3];
+    const float xv[16] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w, e.x, e.y, e.z, e.w, f.x, f.y, f.z, f.w};
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+      float wv[16];
+      unpack16_fp8(t.w[i][j], wv);
+      float v = acc[i];
+#pragma unroll
+      for (int k = 0; k < 16; ++k) v = __builtin_fmaf(wv[k], xv[k], v);
+      acc[i] = on ? v : acc[i];
+    }
+    roll_fence(acc, R);
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+      const int r = nrow[i] >= 0 ? nrow[i] : first;
+      t.w[i][j] = ldw16(W.q + (size_t)r * K + (size_t)cc * 16);
+    }
+    fx_issue_here();
+  }
+  if (nchunk >= 64) {
+#pragma unroll
+    for (int i = 0; i < R; ++i) acc[i] = butterfly64(acc[i]) * t.sc[i];
+  } else {
+    const int nl = lanes_for(nchunk);
+#pragma unroll
+    for (int i = 0; i < R; ++i) acc[i] = butterfly(acc[i], nl) * t.sc[i];
+  }
+  roll_fence(acc, R);
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    t.row[i] = nrow[i];
+    t.sc[i] = W.s[nrow[i] >= 0 ? nrow[i] : first];
+  }
+  fx_issue_here();
+}
+// gemv_pipe_x's walk with rolling dots: t0 holds group `wave` (gemv_prime) and the group WS ahead is
+// requested here. While both tiles have a group two ahead, each dot requests it (unconditionally);
+// the last groups are reduced by tile_dot, as in gemv_pipe_x. The rolling loop is entered only on
+// the path that requested t1, so every path into it has the same loads in flight (the compiler's
+// load counts at the loop head are then exact instead of those of the shortest path).
+template <int WS = FX_WAVES, class TileT, class WT, class RowFn, class XsFn, class EmitFn>
+__device__ __forceinline__ void gemv_pipe_roll(TileT& t0, const WT& W, int K, XsFn xsof, int ngroups, RowFn& rowof,
+                                               EmitFn emit) {
+  TileT t1;
+  float acc[TileT::kRows];
+  int rows[TileT::kRows];
+  int g = wave_id();
+  if (g + 3 * WS < ngroups) {
+    tile_load(t1, W, K, g + WS, rowof);
+    do {
+      tile_dot_roll(t0, xsof(g), K, acc, rows, W, g + 2 * WS, rowof);
+      emit(g, rows, acc);
+      tile_dot_roll(t1, xsof(g + WS), K, acc, rows, W, g + 3 * WS, rowof);
+      emit(g + WS, rows, acc);
+      g += 2 * WS;
+    } while (g + 3 * WS < ngroups);
+  } else if (g + WS < ngroups) {
+    tile_load(t1, W, K, g + WS, rowof);
+  }
+  // t0 holds g, t1 holds g + WS; g + 2 WS (if any) is requested into t0 once t0 is reduced
+  if (g < ngroups) {
+    tile_dot(t0, xsof(g), K, acc);
+    emit(g, t0.row, acc);
+    if (g + WS < ngroups) {
+      const int g2 = g + 2 * WS;
+      if (g2 < ngroups) tile_load(t0, W, K, g2, rowof);
+      tile_dot(t1, xsof(g + WS), K, acc);
+      emit(g + WS, t1.row, acc);
+      if (g2 < ngroups) {
+        tile_dot(t0, xsof(g2), K, acc);
+        emit(g2, t0.row, acc);
+      }
+    }
+  }
+}
 // Walk the wave's groups g = wave, wave + WS, ... (WS: the waves that walk, 0 .. WS - 1); t0 holds
 // group `wave` (gemv_prime). emit(g, rows, acc) sees the R results on every lane (row < 0: no row).
+// FP8 tiles take the rolling walk above (FX_PIPE_ROLL_FP8, default on); bf16 tiles take it only
+// with FX_PIPE_ROLL (default off: measured no faster in the decode, whose bf16 walks are 4 tiles per
+// wave) and otherwise request tile k + 2 after tile k's whole dot (FX_PIPE_DEPTH 2) or rotate three
+// tiles (FX_PIPE_DEPTH 3).
+#ifndef FX_PIPE_ROLL
+#define FX_PIPE_ROLL 0
+#endif
+#ifndef FX_PIPE_ROLL_FP8
+#define FX_PIPE_ROLL_FP8 1
+#endif
 #ifndef FX_PIPE_DEPTH
 #define FX_PIPE_DEPTH 2
 #endif
+template <class TileT>
+struct RollOf {
+  static constexpr bool value = FX_PIPE_ROLL;
+};
+template <int R, int NJ>
+struct RollOf<TileQ<R, NJ>> {
+  static constexpr bool value = FX_PIPE_ROLL_FP8;
+};
 template <int WS = FX_WAVES, class TileT, class WT, class RowFn, class XsFn, class EmitFn>
 __device__ __forceinline__ void gemv_pipe_x(TileT& t0, const WT& W, int K, XsFn xsof, int ngroups, RowFn& rowof,
                                             EmitFn emit) {
+  if constexpr (RollOf<TileT>::value) {
+    gemv_pipe_roll<WS>(t0, W, K, xsof, ngroups, rowof, emit);
+    return;
+  }
   TileT t1;
   float acc[TileT::kRows];
   int g = wave_id();

@@ -422,7 +422,9 @@ __global__ void __launch_bounds__(256) fxp_loaded_kernel(uint32_t* flag, int a, 
 // mode 0: tile_dot (the real dot_lanes work); mode 1: the same loads, each tile folded by one xor
 // per word (no dot); mode 2: as 1 with every load instruction of a tile reading the next KiB of the
 // tile's 16 contiguous KiB (instead of row-interleaved); modes 3, 4: the sliced walk (gemv_slices_x)
-// with 2 / 4 slices (4 rows x 1 KiB) in flight per wave.
+// with 2 / 4 slices (4 rows x 1 KiB) in flight per wave; mode 5: the rolling walk (gemv_pipe_roll:
+// each chunk column of a tile re-filled with the tile two ahead once its fmas are done); modes 6, 7:
+// FP8 rows of K codes (TileQ<4, 2>, the expert stages' FP8 tiles), tile_dot and rolling.
 template <int MODE>
 __device__ __forceinline__ void gemv_walk(const uint16_t* W, int K, int r0, int ngroups, const float* xs, float& sink) {
   auto rowof = [&](int g, int i) { return r0 + g * 4 + i; };
@@ -430,6 +432,20 @@ __device__ __forceinline__ void gemv_walk(const uint16_t* W, int K, int r0, int 
     Tile<4, 4> t0;
     gemv_prime(t0, W, K, ngroups, rowof);
     gemv_pipe(t0, W, K, xs, ngroups, rowof, [&](int, const int*, const float* acc) { sink += acc[0] + acc[1] + acc[2] + acc[3]; });
+  } else if constexpr (MODE == 5) {
+    Tile<4, 4> t0;
+    gemv_prime(t0, W, K, ngroups, rowof);
+    gemv_pipe_roll(t0, W, K, [&](int) { return xs; }, ngroups, rowof,
+                   [&](int, const int*, const float* acc) { sink += acc[0] + acc[1] + acc[2] + acc[3]; });
+  } else if constexpr (MODE == 6 || MODE == 7) {
+    // codes [rows][K] at W (scales: any words of the buffer; only the timing is used)
+    const Fp8W Q{(const uint8_t*)W, (const float*)W};
+    auto rowq = [&](int g, int i) { return r0 + g * 4 + i; };
+    TileQ<4, 2> t0;
+    gemv_prime(t0, Q, K, ngroups, rowq);
+    auto em = [&](int, const int*, const float* acc) { sink += acc[0] + acc[1] + acc[2] + acc[3]; };
+    if constexpr (MODE == 6) gemv_pipe(t0, Q, K, xs, ngroups, rowq, em);
+    else gemv_pipe_roll(t0, Q, K, [&](int) { return xs; }, ngroups, rowq, em);
   } else if constexpr (MODE >= 3) {
     // the sliced walk with 2 (mode 3) or 4 (mode 4) slices of 4 KiB in flight per wave
     constexpr int D = MODE == 3 ? 2 : 4;
@@ -479,7 +495,10 @@ __global__ void __launch_bounds__(256) fxp_gemv_kernel(const uint16_t* W, int K,
   else if (mode == 1) gemv_walk<1>(W, K, r0, ngroups, xs, sink);
   else if (mode == 2) gemv_walk<2>(W, K, r0, ngroups, xs, sink);
   else if (mode == 3) gemv_walk<3>(W, K, r0, ngroups, xs, sink);
-  else gemv_walk<4>(W, K, r0, ngroups, xs, sink);
+  else if (mode == 4) gemv_walk<4>(W, K, r0, ngroups, xs, sink);
+  else if (mode == 5) gemv_walk<5>(W, K, r0, ngroups, xs, sink);
+  else if (mode == 6) gemv_walk<6>(W, K, r0, ngroups, xs, sink);
+  else gemv_walk<7>(W, K, r0, ngroups, xs, sink);
   __syncthreads();
   if (threadIdx.x == 0) ticks[blockIdx.x] = __builtin_amdgcn_s_memrealtime() - t0;
   if (sink == 1234.5f) out[0] = sink;
@@ -802,7 +821,7 @@ int fxp_loaded(int a, int b, uint32_t rounds, int depth, int work, const void* l
 // the GEMV walk over rows_per_block * blocks rows of W [rows][K] (K = 2048, rows_per_block a multiple
 // of 4): per-block ticks and the launch's event time
 int fxp_gemv(const void* W, int K, int rows_per_block, int blocks, int mode, uint64_t* ticks_host, float* ms) {
-  if (K != 2048 || rows_per_block % 4 || mode < 0 || mode > 4 || blocks <= 0) return -1;
+  if (K != 2048 || rows_per_block % 4 || mode < 0 || mode > 7 || blocks <= 0) return -1;
   uint64_t* d_ticks = nullptr;
   float* out = nullptr;
   hipEvent_t e0, e1;
