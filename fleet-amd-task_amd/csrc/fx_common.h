@@ -39,6 +39,7 @@ __device__ __forceinline__ void prof_mark_wave(const FxEnv& e, int slot) {
 
 // LDS layout (bytes)
 #define LDS_XS 0                         // f32 [11264]  GEMV input row
+#define LDS_XS_FLOATS 11264
 #define LDS_RED (45056)                  // f32 [1024]   reductions / small tables
 #define LDS_MISC (LDS_RED + 4096)        // scalars: token, expert, slot weights
 #define LDS_RES (LDS_MISC + 512)         // f32 [128]    residual / output values of the worker's rows

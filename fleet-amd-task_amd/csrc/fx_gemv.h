@@ -764,6 +764,11 @@ __device__ __forceinline__ void op_gemv_w(const fx_stage& s, FxEnv& env, const W
   void* out = (void*)s.out;
   const bool want_max = (s.flags & FX_F_ARGMAX) != 0;
   const bool add_res = residual || res_embed;
+  // The LM head (argmax) keeps its rows' bf16 results in LDS past the input row and stores them
+  // once its walk is done: a store among the walk's weight loads slows the stream (a 400-row walk
+  // per CU: 59.6 us without stores, 64.8 with one per row or per tile). The same bits reach `out`.
+  const bool defer = want_max && !out_ll && (r1 - r0) <= 2 * (LDS_XS_FLOATS - K);
+  uint16_t* lo16 = (uint16_t*)(xs + K);
   float best = -__builtin_inff();
   int best_i = 0x7fffffff;
   wk.run(W, K, xs, ngroups, rowof, [&](int g, const int* row, const float* acc) {
@@ -776,6 +781,8 @@ __device__ __forceinline__ void op_gemv_w(const fx_stage& s, FxEnv& env, const W
       const uint32_t b = f2bf(v);
       if (out_ll) {
         if (lane == 0) rres[FX_MAX_OUT_ROWS / 2 + row[i] - r0] = bf2f(b);
+      } else if (defer) {
+        if (lane == i) lo16[row[i] - r0] = (uint16_t)b;
       } else if (lane == i) {
         stc2(out, (uint32_t)row[i] * 2, b);
       }
@@ -786,6 +793,22 @@ __device__ __forceinline__ void op_gemv_w(const fx_stage& s, FxEnv& env, const W
     }
   });
   prof_mark(env, 5);
+  if (defer) {
+    // rows [r0, r1) as 8-byte stores (r0 is a multiple of 4), the last < 4 rows one by one
+    __syncthreads();
+    const int n = r1 - r0;
+    for (int t = fx_tid(); 4 * t < n; t += FX_THREADS) {
+      const int q = 4 * t;
+      if (q + 4 <= n) {
+        u32x2 v;
+        v.x = (uint32_t)lo16[q] | ((uint32_t)lo16[q + 1] << 16);
+        v.y = (uint32_t)lo16[q + 2] | ((uint32_t)lo16[q + 3] << 16);
+        stc8(out, (uint32_t)(r0 + q) * 2, v);
+      } else {
+        for (int k = q; k < n; ++k) stc2(out, (uint32_t)(r0 + k) * 2, lo16[k]);
+      }
+    }
+  }
   if (out_ll) {
     __syncthreads();
     const float* o = rres + FX_MAX_OUT_ROWS / 2;

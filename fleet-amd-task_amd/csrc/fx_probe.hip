@@ -424,11 +424,51 @@ __global__ void __launch_bounds__(256) fxp_loaded_kernel(uint32_t* flag, int a, 
 // tile's 16 contiguous KiB (instead of row-interleaved); modes 3, 4: the sliced walk (gemv_slices_x)
 // with 2 / 4 slices (4 rows x 1 KiB) in flight per wave; mode 5: the rolling walk (gemv_pipe_roll:
 // each chunk column of a tile re-filled with the tile two ahead once its fmas are done); modes 6, 7:
-// FP8 rows of K codes (TileQ<4, 2>, the expert stages' FP8 tiles), tile_dot and rolling.
+// FP8 rows of K codes (TileQ<4, 2>, the expert stages' FP8 tiles), tile_dot and rolling; modes 8, 9:
+// mode 0 with each row's bf16 result stored to `out` as the LM head stores its logits (one 2-byte
+// sc1 store per row from lane i, mode 8) or as one 8-byte store of the tile's 4 rows (mode 9).
 template <int MODE>
-__device__ __forceinline__ void gemv_walk(const uint16_t* W, int K, int r0, int ngroups, const float* xs, float& sink) {
+__device__ __forceinline__ void gemv_walk(const uint16_t* W, int K, int r0, int ngroups, const float* xs, float& sink,
+                                          void* out) {
   auto rowof = [&](int g, int i) { return r0 + g * 4 + i; };
-  if constexpr (MODE == 0) {
+  if constexpr (MODE == 10) {
+    // the LM head's deferred stores: results into LDS per tile, 8-byte stores after the walk
+    __shared__ uint16_t lo16[400];
+    Tile<4, 4> t0;
+    gemv_prime(t0, W, K, ngroups, rowof);
+    gemv_pipe(t0, W, K, xs, ngroups, rowof, [&](int, const int* row, const float* acc) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (lane_id() == i) lo16[row[i] - r0] = (uint16_t)f2bf(acc[i]);
+    });
+    __syncthreads();
+    const int n = ngroups * 4;
+    for (int t = threadIdx.x; 4 * t < n && 4 * t < 400; t += 256) {
+      u32x2 v;
+      v.x = (uint32_t)lo16[4 * t] | ((uint32_t)lo16[4 * t + 1] << 16);
+      v.y = (uint32_t)lo16[4 * t + 2] | ((uint32_t)lo16[4 * t + 3] << 16);
+      stc8(out, (uint32_t)(r0 + 4 * t) * 2, v);
+    }
+  } else if constexpr (MODE == 8 || MODE == 9) {
+    Tile<4, 4> t0;
+    gemv_prime(t0, W, K, ngroups, rowof);
+    gemv_pipe(t0, W, K, xs, ngroups, rowof, [&](int, const int* row, const float* acc) {
+      const int lane = lane_id();
+      uint32_t b[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) b[i] = f2bf(acc[i]);
+      if constexpr (MODE == 8) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (lane == i) stc2(out, (uint32_t)row[i] * 2, b[i]);
+      } else {
+        u32x2 v;
+        v.x = b[0] | (b[1] << 16);
+        v.y = b[2] | (b[3] << 16);
+        if (lane == 0) stc8(out, (uint32_t)row[0] * 2, v);
+      }
+    });
+  } else if constexpr (MODE == 0) {
     Tile<4, 4> t0;
     gemv_prime(t0, W, K, ngroups, rowof);
     gemv_pipe(t0, W, K, xs, ngroups, rowof, [&](int, const int*, const float* acc) { sink += acc[0] + acc[1] + acc[2] + acc[3]; });
@@ -491,14 +531,17 @@ __global__ void __launch_bounds__(256) fxp_gemv_kernel(const uint16_t* W, int K,
   const int r0 = blockIdx.x * rows_per_block, ngroups = rows_per_block / 4;
   float sink = 0.0f;
   const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
-  if (mode == 0) gemv_walk<0>(W, K, r0, ngroups, xs, sink);
-  else if (mode == 1) gemv_walk<1>(W, K, r0, ngroups, xs, sink);
-  else if (mode == 2) gemv_walk<2>(W, K, r0, ngroups, xs, sink);
-  else if (mode == 3) gemv_walk<3>(W, K, r0, ngroups, xs, sink);
-  else if (mode == 4) gemv_walk<4>(W, K, r0, ngroups, xs, sink);
-  else if (mode == 5) gemv_walk<5>(W, K, r0, ngroups, xs, sink);
-  else if (mode == 6) gemv_walk<6>(W, K, r0, ngroups, xs, sink);
-  else gemv_walk<7>(W, K, r0, ngroups, xs, sink);
+  if (mode == 0) gemv_walk<0>(W, K, r0, ngroups, xs, sink, out);
+  else if (mode == 1) gemv_walk<1>(W, K, r0, ngroups, xs, sink, out);
+  else if (mode == 2) gemv_walk<2>(W, K, r0, ngroups, xs, sink, out);
+  else if (mode == 3) gemv_walk<3>(W, K, r0, ngroups, xs, sink, out);
+  else if (mode == 4) gemv_walk<4>(W, K, r0, ngroups, xs, sink, out);
+  else if (mode == 5) gemv_walk<5>(W, K, r0, ngroups, xs, sink, out);
+  else if (mode == 6) gemv_walk<6>(W, K, r0, ngroups, xs, sink, out);
+  else if (mode == 7) gemv_walk<7>(W, K, r0, ngroups, xs, sink, out);
+  else if (mode == 8) gemv_walk<8>(W, K, r0, ngroups, xs, sink, out);
+  else if (mode == 9) gemv_walk<9>(W, K, r0, ngroups, xs, sink, out);
+  else gemv_walk<10>(W, K, r0, ngroups, xs, sink, out);
   __syncthreads();
   if (threadIdx.x == 0) ticks[blockIdx.x] = __builtin_amdgcn_s_memrealtime() - t0;
   if (sink == 1234.5f) out[0] = sink;
@@ -821,13 +864,15 @@ int fxp_loaded(int a, int b, uint32_t rounds, int depth, int work, const void* l
 // the GEMV walk over rows_per_block * blocks rows of W [rows][K] (K = 2048, rows_per_block a multiple
 // of 4): per-block ticks and the launch's event time
 int fxp_gemv(const void* W, int K, int rows_per_block, int blocks, int mode, uint64_t* ticks_host, float* ms) {
-  if (K != 2048 || rows_per_block % 4 || mode < 0 || mode > 7 || blocks <= 0) return -1;
+  if (K != 2048 || rows_per_block % 4 || mode < 0 || mode > 10 || blocks <= 0) return -1;
+  if (mode == 10 && rows_per_block > 400) return -1;
   uint64_t* d_ticks = nullptr;
   float* out = nullptr;
   hipEvent_t e0, e1;
   hipError_t e;
   if ((e = hipMalloc(&d_ticks, 8 * blocks)) != hipSuccess) return e;
-  if ((e = hipMalloc(&out, 64)) != hipSuccess) return e;
+  // the walks' outputs (modes 8, 9: one bf16 per row)
+  if ((e = hipMalloc(&out, (size_t)rows_per_block * blocks * 2 + 64)) != hipSuccess) return e;
   (void)hipEventCreate(&e0);
   (void)hipEventCreate(&e1);
   (void)hipEventRecord(e0, 0);

@@ -67,7 +67,8 @@ def main():
                     help="only the decode GEMV walk (Tile<4, 4>, K = 2048) against the same loads without the dot")
     ap.add_argument("--gemv-modes", default="0,3,4,1",
                     help="the walks --gemv times: 0 tile_dot, 1 xor only, 2 contiguous xor, 3/4 sliced, 5 rolling, "
-                         "6 FP8 tile_dot, 7 FP8 rolling")
+                         "6 FP8 tile_dot, 7 FP8 rolling, 8/9 tile_dot with per-row / per-tile stores of the results, "
+                         "10 with the results stored after the walk")
     ap.add_argument("--loaded", action="store_true",
                     help="only the sc1 flag round trip against the depth of a concurrent full-chip stream")
     ap.add_argument("--reuse", action="store_true",
@@ -123,7 +124,10 @@ def main():
         print("|---|---|---|---|---|---|", flush=True)
         names = {0: "tile_dot (decode GEMV)", 1: "same loads, xor only", 2: "contiguous KiB order, xor only",
                  3: "sliced, 2 slices in flight", 4: "sliced, 4 slices in flight",
-                 5: "rolling tile_dot", 6: "FP8 tile_dot (TileQ<4, 2>)", 7: "FP8 rolling tile_dot"}
+                 5: "rolling tile_dot", 6: "FP8 tile_dot (TileQ<4, 2>)", 7: "FP8 rolling tile_dot",
+                 8: "tile_dot + a 2-byte store per row (the LM head's logits)",
+                 9: "tile_dot + one 8-byte store per tile",
+                 10: "tile_dot, results into LDS, 8-byte stores after the walk"}
         modes = [int(m) for m in args.gemv_modes.split(",")]
         for rpb in (400, 100, 36):
             for mode in modes:
@@ -132,7 +136,7 @@ def main():
                     assert L.fxp_stream(ctypes.c_void_p(cold.ptr), cold.nbytes // 256, 256, 256, 8, 0, ticks, ctypes.byref(ms)) == 0
                     assert L.fxp_gemv(ctypes.c_void_p(W.ptr), 2048, rpb, 256, mode, ticks, ctypes.byref(ms)) == 0
                 t = np.array(ticks[:256], np.float64) * TICK_NS / 1e3
-                nb = rpb * 2048 * (1 if mode >= 6 else 2)
+                nb = rpb * 2048 * (1 if mode in (6, 7) else 2)
                 print(f"| {names[mode]} | {rpb} | {nb / 2**20:.2f} | {256 * nb / (ms.value * 1e6):.0f} | "
                       f"{np.median(t):.2f} | {t.max():.2f} |", flush=True)
         rt.close()
