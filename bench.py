@@ -70,6 +70,11 @@ def traffic_per_token(ctx):
     return t["bytes_per_dispatch"] / t.get("iters_per_dispatch", 1)
 
 
+def config_name(ctx):
+    """The BASELINE.json config a context length is quoted on: configs[3] at 1,024, configs[4] at 16,384."""
+    return {1024: "BASELINE configs[3]", 16384: "BASELINE configs[4]"}.get(ctx, f"BASELINE configs[3] at ctx {ctx}")
+
+
 def cpu_baseline(rt, runner, bufs, plan, prompt, ctx, n_tok, gpu_ids):
     """Time the oracle on the host decoding n_tok tokens from position ctx - 1 with the GPU prefill's
     cache rows 0..ctx-2 (test infrastructure: the checker, run here only as the reported baseline)."""
@@ -262,8 +267,8 @@ def main():
         "data": "synthetic: seeded N(0,0.02) bf16 weights" + (
             " (experts and LM head quantized to FP8, per-row scales)" if args.fp8_head else
             " (experts quantized to FP8, per-row scales)" if args.fp8_experts else "")
-                + ", seeded uniform 1024-token prompt",
-        "config": {"workload": "BASELINE configs[3]: DeepSeek-V2-Lite 27 layers, 1024-token prompt (prefill untimed), "
+                + f", seeded uniform {ctx}-token prompt",
+        "config": {"workload": f"{config_name(ctx)}: DeepSeek-V2-Lite 27 layers, {ctx}-token prompt (prefill untimed), "
                                "greedy decode at batch 1", "layers": d.L, "batch": 1, "ctx": ctx, "decode_tokens": K,
                    "splits": plan.n_splits, "split": plan.split, "attn": plan.attn, "pair": plan.pair, "seed": args.seed, "fp8_experts": args.fp8_experts,
                    "fp8_head": args.fp8_head},
