@@ -5,7 +5,14 @@
 // are both spread over every worker for every slot (pair groups / 8 output rows each), shared slots
 // first; the combine of a row happens where its eight slot values are.
 #pragma once
+#include <type_traits>
+
 #include "fx_gemv.h"
+
+// bf16 expert gate|up: routed groups walked as tiles of one gate/up pair with the rolling walk
+#ifndef FX_W13_ROW2
+#define FX_W13_ROW2 1
+#endif
 
 #define FX_SLOTS 8
 
@@ -240,8 +247,23 @@ __device__ __forceinline__ void w13_main(const fx_stage& s, FxEnv& env, const WT
   typename TileT::Row tq;
   auto rowQ = [&](int, int) { return rowB(nB4, wave_id()); };
   if (nB4 < nB) tile_load(tq, W, K, 0, rowQ);
-  gemv_prime(t0, W, K, nB4, rowB);
-  gemv_pipe(t0, W, K, xs, nB4, rowB, [&](int g, const int* row, const float* acc) { emit(nA, g, acc); });
+  if constexpr (FX_W13_ROW2 && std::is_same<TileT, Tile<4, 4>>::value) {
+    // bf16: the routed groups walked as tiles of one pair (gate p, up p; half of a group, 8 KiB per
+    // wave) by the rolling walk: a worker's routed share is a short stream, which smaller tiles
+    // with the next tile requested during the dot finish sooner. Pair g2 is half g2 & 1 of group
+    // g2 >> 1; its act value is emit's for that half.
+    auto rowB2 = [&](int g2, int i) { return rowB(g2 >> 1, ((g2 & 1) << 1) | i); };
+    Tile<2, 4> u0;
+    gemv_prime(u0, W, K, 2 * nB4, rowB2);
+    gemv_pipe_roll(u0, W, K, [&](int) { return (const float*)xs; }, 2 * nB4, rowB2,
+                   [&](int g2, const int* row, const float* acc) {
+                     const float a = silu_s(bf16r(acc[0])) * bf16r(acc[1]);
+                     if (lane_id() == 0) actl[2 * (nA + (g2 >> 1)) + (g2 & 1)] = a;
+                   });
+  } else {
+    gemv_prime(t0, W, K, nB4, rowB);
+    gemv_pipe(t0, W, K, xs, nB4, rowB, [&](int g, const int* row, const float* acc) { emit(nA, g, acc); });
+  }
   if (nB4 < nB) {
     float acc[1];
     tile_dot(tq, xs, K, acc);
