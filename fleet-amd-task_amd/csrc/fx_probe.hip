@@ -428,12 +428,21 @@ __global__ void __launch_bounds__(256) fxp_loaded_kernel(uint32_t* flag, int a, 
 // mode 0 with each row's bf16 result stored to `out` as the LM head stores its logits (one 2-byte
 // sc1 store per row from lane i, mode 8) or as one 8-byte store of the tile's 4 rows (mode 9); mode
 // 10: results into LDS, 8-byte stores after the walk; modes 11, 12: tiles of 2 rows, two-tile and
-// rolling walks.
+// rolling walks; modes 13, 14: tiles of 1 row, rolling and two-tile walks.
 template <int MODE>
 __device__ __forceinline__ void gemv_walk(const uint16_t* W, int K, int r0, int ngroups, const float* xs, float& sink,
                                           void* out) {
   auto rowof = [&](int g, int i) { return r0 + g * 4 + i; };
-  if constexpr (MODE == 11 || MODE == 12) {
+  if constexpr (MODE == 13 || MODE == 14) {
+    // tiles of 1 row (4 KiB per wave): rolling (13) and two-tile (14) walks
+    auto row1 = [&](int g, int i) { return r0 + g; };
+    Tile<1, 4> t0;
+    const int ng1 = ngroups * 4;
+    gemv_prime(t0, W, K, ng1, row1);
+    auto em = [&](int, const int*, const float* acc) { sink += acc[0]; };
+    if constexpr (MODE == 14) gemv_pipe(t0, W, K, xs, ng1, row1, em);
+    else gemv_pipe_roll(t0, W, K, [&](int) { return xs; }, ng1, row1, em);
+  } else if constexpr (MODE == 11 || MODE == 12) {
     // tiles of 2 rows (8 KiB per wave): the two-tile walk (11) and the rolling walk (12)
     auto row2 = [&](int g, int i) { return r0 + g * 2 + i; };
     Tile<2, 4> t0;
@@ -554,7 +563,9 @@ __global__ void __launch_bounds__(256) fxp_gemv_kernel(const uint16_t* W, int K,
   else if (mode == 9) gemv_walk<9>(W, K, r0, ngroups, xs, sink, out);
   else if (mode == 10) gemv_walk<10>(W, K, r0, ngroups, xs, sink, out);
   else if (mode == 11) gemv_walk<11>(W, K, r0, ngroups, xs, sink, out);
-  else gemv_walk<12>(W, K, r0, ngroups, xs, sink, out);
+  else if (mode == 12) gemv_walk<12>(W, K, r0, ngroups, xs, sink, out);
+  else if (mode == 13) gemv_walk<13>(W, K, r0, ngroups, xs, sink, out);
+  else gemv_walk<14>(W, K, r0, ngroups, xs, sink, out);
   __syncthreads();
   if (threadIdx.x == 0) ticks[blockIdx.x] = __builtin_amdgcn_s_memrealtime() - t0;
   if (sink == 1234.5f) out[0] = sink;
@@ -877,7 +888,7 @@ int fxp_loaded(int a, int b, uint32_t rounds, int depth, int work, const void* l
 // the GEMV walk over rows_per_block * blocks rows of W [rows][K] (K = 2048, rows_per_block a multiple
 // of 4): per-block ticks and the launch's event time
 int fxp_gemv(const void* W, int K, int rows_per_block, int blocks, int mode, uint64_t* ticks_host, float* ms) {
-  if (K != 2048 || rows_per_block % 4 || mode < 0 || mode > 12 || blocks <= 0) return -1;
+  if (K != 2048 || rows_per_block % 4 || mode < 0 || mode > 14 || blocks <= 0) return -1;
   if (mode == 10 && rows_per_block > 400) return -1;
   uint64_t* d_ticks = nullptr;
   float* out = nullptr;

@@ -69,7 +69,7 @@ def main():
     ap.add_argument("--gemv-modes", default="0,3,4,1",
                     help="the walks --gemv times: 0 tile_dot, 1 xor only, 2 contiguous xor, 3/4 sliced, 5 rolling, "
                          "6 FP8 tile_dot, 7 FP8 rolling, 8/9 tile_dot with per-row / per-tile stores of the results, "
-                         "10 with the results stored after the walk, 11/12 tiles of 2 rows (two-tile / rolling)")
+                         "10 with the results stored after the walk, 11/12 tiles of 2 rows (two-tile / rolling), 13/14 tiles of 1 row (rolling / two-tile)")
     ap.add_argument("--loaded", action="store_true",
                     help="only the sc1 flag round trip against the depth of a concurrent full-chip stream")
     ap.add_argument("--reuse", action="store_true",
@@ -129,7 +129,8 @@ def main():
                  8: "tile_dot + a 2-byte store per row (the LM head's logits)",
                  9: "tile_dot + one 8-byte store per tile",
                  10: "tile_dot, results into LDS, 8-byte stores after the walk",
-                 11: "tile_dot, tiles of 2 rows", 12: "rolling tile_dot, tiles of 2 rows"}
+                 11: "tile_dot, tiles of 2 rows", 12: "rolling tile_dot, tiles of 2 rows",
+                 13: "rolling tile_dot, tiles of 1 row", 14: "tile_dot, tiles of 1 row"}
         modes = [int(m) for m in args.gemv_modes.split(",")]
         for rpb in [int(r) for r in args.gemv_rows.split(",")]:
             for mode in modes:
