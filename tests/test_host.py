@@ -176,8 +176,9 @@ def test_host_philox_and_tables_match_oracle():
     assert np.array_equal(c1, c2) and np.array_equal(s1, s2)
 
 
-def test_bytes_per_token_matches_survey():
-    # 4,934,724,608 B at the first token (ctx 1024), 5,412,482,048 B at ctx 16,384
+def test_bytes_per_token_matches_the_hand_count():
+    # weights read once per token (4,902,874,112 B with the norms) + 27 x 1,152 B of latent cache per
+    # attended position: 4,934,724,608 B at the first token (ctx 1024), 5,412,482,048 B at ctx 16,384
     assert P.bytes_per_token(P.REAL_DIMS, 1024) == 4_934_724_608
     assert P.bytes_per_token(P.REAL_DIMS, 16384) == 5_412_482_048
     assert P.packed_bytes(P.REAL_DIMS) == 31_412_968_448
