@@ -384,6 +384,41 @@ def test_router_experts_combine(rt):
         assert np.array_equal(cpu, bufs["W2_1"].download_range(e * H * I, H * I).reshape(H, I))
 
 
+@pytest.mark.parametrize("I", [512, 1024, 1400])
+def test_expert_gate_up_walk_lengths(rt, I):
+    """The expert gate|up stage at other intermediate sizes, over the same seeded expert buffer cut
+    into experts of 2 I rows: the routed walk of a worker then has 6 (I = 512: three pair tiles per
+    wave, the walk's tail only), 12 (I = 1,024: one rolling round and the tail) or 16-17 (I = 1,400:
+    the rolling loop, and the leftover group split by rows) groups instead of the real 16-17 at I =
+    1,408, and the shared walk 2, 4 or 5-6. Bit-exact against the oracle's moe_w13_silu on the same
+    slabs and routing."""
+    rng = np.random.default_rng(16)
+    d = P.REAL_DIMS
+    E = d.E
+    print(f"[w13 walk] I={I}", flush=True)
+    bufs = P.fill_seeded(rt, d, SEED, layers=2, head=False, keys={"W_gate_1", "W13_1"})
+    _KEEP.extend(bufs.values())
+    x = rng_bf16(rng, H)
+    nw = rng_bf16(rng, H, 0.5)
+    dx, dn = pk(rt, x), dev(rt, nw, "bf16")
+    h, logits, topk_w, routing, mask = O.moe_router(x, bufs["W_gate_1"].download(), norm_w=nw)
+    lx = pk(rt, logits, "pk32", tag=TOUT)
+    outs = {n: sentinel(rt, sh, t) for n, sh, t in [("topk_w", (8,), "f32"), ("routing", (E + 2,), "i32"),
+                                                   ("mask", (E + 3,), "i32"), ("logits", (E,), "f32")]}
+    act8 = pk_out(rt, (8, I))
+    st = R.FxStage().set(op=R.FX_OP_MOE_W13, n_rows=I, k=H, n_slots=8, topk=d.TOPK, n_forced=2, scaling=1.0,
+                         aux_i0=E, aux_i1=26, prow=4, layer=1, eps=1e-6, x=dx.ptr, w_norm=dn.ptr,
+                         w=bufs["W13_1"].ptr, out=act8.ptr, src=[SIDX, SRC, 0, 0],
+                         aux={0: lx.ptr, 1: outs["topk_w"].ptr, 2: outs["routing"].ptr, 3: outs["mask"].ptr,
+                              4: outs["logits"].ptr})
+    rt.run_stage(st, tbase=TB, sidx=SIDX + 1)
+    assert np.array_equal(outs["mask"].download(), mask)
+    ids = [int(e) for e in mask[:8]]
+    W13 = np.stack([bufs["W13_1"].download_range(e * 2 * I * H, 2 * I * H).reshape(2 * I, H) for e in ids])
+    e_act = O.moe_w13_silu(h, W13, np.arange(9, dtype=np.int32), 8)
+    assert mismatch(act8.download(tag=TOUT + 1), e_act) == 0
+
+
 def test_dense_gate_up(rt):
     rng = np.random.default_rng(7)
     d = P.REAL_DIMS
