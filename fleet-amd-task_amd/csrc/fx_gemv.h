@@ -895,8 +895,12 @@ __device__ __forceinline__ void op_dense_gu(const fx_stage& s, FxEnv& env) {
   rowof.p1 = 2 * q1;
   rowof.I = I;
   const int ngroups = q1 - q0;
-  Tile<4, 4> t0;
-  gemv_prime(t0, W, K, ngroups, rowof);
+  // the worker's 2 (q1 - q0) pairs (an even count: every tile's rows exist) walked as tiles of one
+  // gate/up pair by the rolling walk, as the expert gate|up stage's routed groups: pair g2 is
+  // p0 + g2, half g2 & 1 of group g2 >> 1
+  auto rowof2 = [&](int g2, int i) { return rowof(g2 >> 1, ((g2 & 1) << 1) | i); };
+  Tile<2, 4> t0;
+  gemv_prime(t0, W, K, 2 * ngroups, rowof2);
   const NormW nw = K <= 8 * FX_THREADS ? norm_prefetch((const uint16_t*)s.w_norm, K) : NormW{};
   poll_row(xs, (const void*)s.x, K, tag_in(s, env, 0), env.err);
   prof_mark(env, 1);
@@ -906,14 +910,12 @@ __device__ __forceinline__ void op_dense_gu(const fx_stage& s, FxEnv& env) {
   const uint32_t tag = tag_out(env);
   // act values of the worker's groups into LDS, published after the stream
   float* actl = (float*)(env.lds + LDS_RES);
-  gemv_pipe(t0, W, K, xs, ngroups, rowof, [&](int g, const int* row, const float* acc) {
-#pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      const float gv = bf16r(acc[2 * q]);
-      const float uv = bf16r(acc[2 * q + 1]);
-      if (lane_id() == 0) actl[2 * g + q] = row[2 * q] >= 0 ? silu_s(gv) * uv : 0.0f;
-    }
-  });
+  gemv_pipe_roll(t0, W, K, [&](int) { return (const float*)xs; }, 2 * ngroups, rowof2,
+                 [&](int g2, const int* row, const float* acc) {
+                   const float gv = bf16r(acc[0]);
+                   const float uv = bf16r(acc[1]);
+                   if (lane_id() == 0) actl[g2] = row[0] >= 0 ? silu_s(gv) * uv : 0.0f;
+                 });
   __syncthreads();
   if (fx_tid() < ngroups)
     pk_put(act, (uint32_t)(q0 + fx_tid()), pack2(actl[2 * fx_tid()], actl[2 * fx_tid() + 1]), tag);
